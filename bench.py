@@ -1,0 +1,247 @@
+#!/usr/bin/env python3
+"""Benchmark of the persistent expert-grouped GEMM on one MI355X.
+
+A step is one ``persistent_grouped_gemm`` call (the full drop-in API: offsets
+already on the device, output allocation, launch) over the BASELINE metric's
+workload: E=16 experts x 512 routed tokens, K=2048, N=4096, bf16 in, fp32
+accumulate, bf16 out.  Inputs are synthetic (N(0,1) activations, N(0,1/K)
+weights) and resident in HBM before the timed region.
+
+Prints ONE JSON line.  ``value`` is TFLOP/s over the timed steps (wall clock
+between two device synchronisations, algorithmic FLOPs 2*M*K*N);
+``roofline.achieved`` is the same FLOPs over the kernel's mean launch time from
+HIP events on the launch stream.  Extra fields compare striped and atomic
+scheduling under uniform and skewed routing, a cache-cold launch time, the
+per-expert torch loop on the GPU, and the CPU oracle on the host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "moe-overlap_amd"))
+sys.path.insert(0, str(REPO))
+
+METRIC = "grouped GEMM TFLOP/s + % bf16 MFMA peak, E=16 512 tok/expert K2048 N4096"
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0
+KERNEL_NAME = "grouped_gemm_kernel<256,256,Bf16>"
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--workload", default="uniform", choices=["uniform", "skewed", "cpu_plumbing"])
+    p.add_argument("--mode", default="atomic", choices=["atomic", "striped"])
+    p.add_argument("--block-m", type=int, default=256)
+    p.add_argument("--block-n", type=int, default=256)
+    p.add_argument("--num-sms", type=int, default=None)
+    p.add_argument("--no-compare", action="store_true", help="skip the schedule/routing comparison")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU oracle sample budget")
+    p.add_argument("--profile-only", action="store_true",
+                   help="only the warmup and timed steps (for rocprofv3 runs)")
+    return p.parse_args()
+
+
+def event_times_ms(fn, iters, flush=None):
+    """Per-launch durations (ms) from HIP events on the current stream."""
+    import torch
+
+    times = []
+    for _ in range(iters):
+        if flush is not None:
+            flush()
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        times.append((s, e))
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in times]
+
+
+def median(xs):
+    ys = sorted(xs)
+    return ys[len(ys) // 2] if ys else float("nan")
+
+
+def cpu_baseline(case, budget_s):
+    """The oracle's per-expert fp32 loop on the host cores, on a sample of experts."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+
+    from oracle import grouped_gemm_oracle as orc
+
+    a = case.a.float().cpu().numpy()
+    b = case.b.float().cpu().numpy()
+    offs = orc.expert_offsets_from_recv_counts(case.counts.numpy())
+    nonempty = [e for e in range(case.num_experts) if offs[e + 1] > offs[e]]
+    flops = 0
+    done = []
+    t0 = time.perf_counter()
+    out = np.empty((a.shape[0], b.shape[2]), np.float32)
+    while time.perf_counter() - t0 < budget_s and len(done) < len(nonempty):
+        e = nonempty[len(done)]
+        sub = np.zeros_like(offs)
+        sub[e + 1:] = offs[e + 1] - offs[e]
+        s, t = int(offs[e]), int(offs[e + 1])
+        orc.grouped_gemm(a[s:t], b[e:e + 1], [0, t - s], out=out[s:t])
+        flops += 2 * (t - s) * case.k * case.n
+        done.append(e)
+    dt = time.perf_counter() - t0
+    threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    return {
+        "value": round(flops / dt / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"{len(done)} of {len(nonempty)} experts of the {case.name} workload "
+                  f"({flops / 1e9:.1f} GFLOP, fp32 numpy per-expert loop, {dt:.1f} s)",
+        "host_cpus": os.cpu_count(),
+        "cpu_model": platform.processor() or platform.machine(),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the grouped GEMM shards by expert; see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import grouped_gemm as gg
+    import workloads
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    case = workloads.make_case(args.workload, device=dev, dtype=torch.bfloat16)
+    offs = gg.expert_offsets_from_recv_counts(case.counts, device=dev)
+    atomic = args.mode == "atomic"
+    kw = dict(num_sms=args.num_sms, block_m=args.block_m, block_n=args.block_n,
+              use_atomic_queue=atomic)
+
+    def step():
+        return gg.persistent_grouped_gemm(case.a, case.b, offs, **kw)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record()
+        step()
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    if args.profile_only:
+        print(json.dumps({"profile_only": True, "ms_per_step": wall / args.steps * 1e3}))
+        return
+
+    flops = case.flops
+    value = flops * args.steps / wall / 1e12
+    k_mean = sum(kernel_ms) / len(kernel_ms)
+    achieved = flops / (k_mean * 1e-3) / 1e12
+
+    # Correctness of the timed configuration against an fp32 torch loop.
+    c = step()
+    ref = gg.reference_grouped_gemm(case.a.float(), case.b.float(), offs)
+    max_abs = (c.float() - ref).abs().max().item()
+    del ref
+    tolerance = 2e-2 * math.sqrt(case.k / 512)
+
+    extra = {}
+    if not args.no_compare:
+        # Cache-cold launches: a 512 MiB write evicts L2 and the 256 MB MALL.
+        scratch = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
+        cold = event_times_ms(step, 10, flush=lambda: scratch.fill_(1.0))
+        extra["cold_kernel_ms_median"] = round(median(cold), 4)
+        extra["cold_tflops"] = round(flops / (median(cold) * 1e-3) / 1e12, 1)
+        del scratch
+        sched = {}
+        for wl in ("uniform", "skewed"):
+            cs = case if wl == args.workload else workloads.make_case(wl, device=dev)
+            o = gg.expert_offsets_from_recv_counts(cs.counts, device=dev)
+            for mode in ("striped", "atomic"):
+                fn = lambda: gg.persistent_grouped_gemm(
+                    cs.a, cs.b, o, num_sms=args.num_sms, block_m=args.block_m,
+                    block_n=args.block_n, use_atomic_queue=(mode == "atomic"))
+                event_times_ms(fn, 3)
+                t = event_times_ms(fn, 20)
+                sched[f"{wl}_{mode}"] = {
+                    "kernel_ms_median": round(median(t), 4), "kernel_ms_min": round(min(t), 4),
+                    "tflops": round(cs.flops / (median(t) * 1e-3) / 1e12, 1)}
+            if cs is not case:
+                del cs
+        extra["schedules"] = sched
+        # The reference API's per-expert torch loop on the GPU (hipBLASLt GEMMs).
+        loop = lambda: gg.reference_grouped_gemm(case.a, case.b, offs)
+        event_times_ms(loop, 2)
+        tl = event_times_ms(loop, 5)
+        extra["torch_loop_gpu_ms_median"] = round(median(tl), 4)
+        extra["torch_loop_gpu_tflops"] = round(flops / (median(tl) * 1e-3) / 1e12, 1)
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(case, args.cpu_seconds)
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,1) tokens, N(0,1/K) weights, random init)",
+        "config": {
+            "workload": f"{case.name}: E={case.num_experts}, M={case.m}, K={case.k}, N={case.n}",
+            "mode": args.mode,
+            "block_m": args.block_m,
+            "block_n": args.block_n,
+            "num_sms": args.num_sms or "all CUs",
+            "queue": "device",
+        },
+        "pct_bf16_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "kernel_ms_mean": round(k_mean, 5),
+        "kernel_ms_min": round(min(kernel_ms), 5),
+        "max_abs_diff_vs_fp32": round(max_abs, 6),
+        "tolerance": round(tolerance, 6),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+            "kernel": KERNEL_NAME if (args.block_m, args.block_n) == (256, 256) else "grouped_gemm_kernel",
+            "algorithmic_flops_per_launch": flops,
+            "algorithmic_bytes_per_launch": case.algorithmic_bytes(),
+            "hbm_gbps_at_algorithmic_bytes": round(case.algorithmic_bytes() / (k_mean * 1e-3) / 1e9, 1),
+        },
+        "cpu_baseline": cpu,
+        **extra,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,135 @@
+/*
+ * mgg.h - C ABI of the MI355X (gfx950) expert-grouped GEMM library (libmgg.so).
+ *
+ * Plain pointers, sizes and a HIP stream passed as void*.  No torch or C++
+ * types cross this boundary and no C++ exception escapes it: every entry point
+ * returns MGG_OK or an error code, and mgg_last_error() returns a message for
+ * the calling thread's most recent failure.
+ *
+ * Device pointers are borrowed for the duration of the (asynchronous) launch
+ * only; the library never frees caller memory.  All work is enqueued on the
+ * given stream; nothing here synchronises the device.
+ *
+ * Reference interface replaced by each entry point (paths relative to the
+ * Hongyu15/moe-overlap checkout):
+ *   mgg_expert_offsets_from_counts -> src/triton_grouped_gemm.py:300-323
+ *                                     (expert_offsets_from_recv_counts)
+ *   mgg_build_work_queue           -> src/triton_grouped_gemm.py:240-297
+ *                                     (_build_work_queue, device part)
+ *   mgg_grouped_gemm               -> src/triton_grouped_gemm.py:326-443
+ *                                     (persistent_grouped_gemm launch), with the
+ *                                     tile kernels of :36-233
+ *   mgg_device_cu_count            -> the `num_sms` grid size the reference
+ *                                     passes by hand (:330, :375)
+ */
+#ifndef MGG_H_
+#define MGG_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define MGG_OK 0
+#define MGG_ERR_INVALID 1     /* bad argument (shape, size, alignment, pointer) */
+#define MGG_ERR_UNSUPPORTED 2 /* valid request outside what the kernels cover   */
+#define MGG_ERR_HIP 3         /* HIP runtime call failed                        */
+
+/* Element types of the GEMM operands. */
+#define MGG_DTYPE_BF16 0
+#define MGG_DTYPE_FP16 1
+
+/* Integer types of the per-expert count vector. */
+#define MGG_INT32 0
+#define MGG_INT64 1
+
+/* Library ABI version (bumped on any signature change). */
+int mgg_abi_version(void);
+
+/* Message for the calling thread's most recent failed call ("" if none). */
+const char* mgg_last_error(void);
+
+/* Number of compute units of HIP device `device` (256 on MI355X). */
+int mgg_device_cu_count(int device, int* cu_count);
+
+/*
+ * offsets[0] = 0, offsets[i+1] = offsets[i] + (int32)counts[i], i < E.
+ * `counts` is int32 or int64 (counts_type) on the device; each count is first
+ * narrowed to int32 (two's-complement wrap), as `.to(torch.int32)` does.
+ * `offsets` is int32 (out_type MGG_INT32, sums wrap modulo 2^32) or int64
+ * (MGG_INT64, exact), length E+1.  E == 0 writes offsets = [0].
+ */
+int mgg_expert_offsets_from_counts(const void* counts, int counts_type, int64_t num_experts,
+                                   void* offsets, int out_type, void* stream);
+
+/*
+ * Fill the tile work queue for `expert_offsets` (int32, length E+1, device):
+ * for each expert e in order, count_e = max(off[e+1]-off[e], 0),
+ * tm_e = ceil(count_e / block_m), tn = ceil(n_size / block_n), and items
+ * (e, tm, tn) for tm < tm_e, tn < tn in row-major order (tile_n fastest).
+ * `num_work` must equal sum_e tm_e * tn (the caller computes it); the three
+ * int32 output arrays have num_work entries.  E must be <= 8192.
+ */
+int mgg_build_work_queue(const int32_t* expert_offsets, int64_t num_experts, int64_t n_size,
+                         int block_m, int block_n, int32_t* work_expert, int32_t* work_tile_m,
+                         int32_t* work_tile_n, int64_t num_work, void* stream);
+
+/*
+ * Host-memory variants of the two builders above, for counts/offsets that
+ * live in CPU memory (the reference's torch ops accept CPU tensors too).
+ * Same arguments and results; they run synchronously on the calling thread.
+ */
+int mgg_expert_offsets_from_counts_host(const void* counts, int counts_type, int64_t num_experts,
+                                        void* offsets, int out_type);
+int mgg_build_work_queue_host(const int64_t* expert_offsets, int64_t num_experts, int64_t n_size,
+                              int block_m, int block_n, int32_t* work_expert,
+                              int32_t* work_tile_m, int32_t* work_tile_n, int64_t num_work);
+
+/*
+ * Persistent grouped GEMM:  C[off[e]+i, :] = A[off[e]+i, :] @ B[e]  for
+ * 0 <= i < max(off[e+1]-off[e], 0), every expert e, fp32 accumulation, output
+ * in the input dtype (round to nearest even).
+ *
+ *   a  [M, K]     row stride lda   (elements; unit inner stride)
+ *   b  [E, K, N]  expert stride ldb_e, row stride ldb_k (unit inner stride)
+ *   c  [M, N]     row stride ldc
+ *   expert_offsets  int32 [E+1] on the device
+ *
+ * Work items are BLOCK_M x BLOCK_N output tiles in the queue order above.
+ * work_expert/work_tile_m/work_tile_n (num_work entries, from
+ * mgg_build_work_queue) are used when num_work >= 0; with num_work < 0 and
+ * null queue pointers, the kernel derives the identical queue from the
+ * offsets on the device (no host round trip).
+ *
+ * num_workers persistent workgroups are launched (<= 0 means one per CU).
+ * use_atomic_queue = 0: worker w takes items w, w+G, w+2G, ... (workers are
+ * numbered so that each XCD owns a contiguous slice of every round).
+ * use_atomic_queue = 1: workers take the next item with atomicAdd on a global
+ * int32 counter owned by the library, one per (device, stream), which starts
+ * every launch at zero and is returned to zero by the last worker to exit.
+ * If work_counter is non-null (device int32) it receives that counter's final
+ * value, num_work + G (each worker over-fetches once), which is the value the
+ * reference leaves in its work_counter (:379-416); with an empty queue it is
+ * left untouched, as there.  Calls on one stream are ordered; calls on
+ * different streams use different counters.
+ *
+ * If the queue is empty, C is zero-filled.  Rows of C not covered by any
+ * expert range are left unwritten.  Supported: dtype BF16/FP16,
+ * block_m, block_n in {64, 128, 256}, K % 8 == 0, N % 8 == 0, strides
+ * multiples of 8 elements, 16-byte aligned base pointers, E <= 2048 when the
+ * queue is derived on the device.
+ */
+int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
+                     const int32_t* expert_offsets, int64_t m_size, int64_t k_size, int64_t n_size,
+                     int64_t num_experts, int64_t lda, int64_t ldb_e, int64_t ldb_k, int64_t ldc,
+                     const int32_t* work_expert, const int32_t* work_tile_m,
+                     const int32_t* work_tile_n, int64_t num_work, int block_m, int block_n,
+                     int num_workers, int use_atomic_queue, int32_t* work_counter, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MGG_H_ */

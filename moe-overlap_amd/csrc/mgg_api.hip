@@ -1,0 +1,260 @@
+// extern "C" entry points of libmgg.so (declared in include/mgg.h): argument
+// validation, library-owned dequeue counters, and the launches.  No C++
+// exception crosses this boundary; failures return a status code and leave a
+// message for mgg_last_error().
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+
+#include "mgg.h"
+#include "mgg_internal.h"
+
+namespace mgg {
+namespace {
+
+thread_local std::string g_last_error;
+
+// Library-owned {counter, done} pairs, one per (device, stream).  Each lives
+// until the process ends; the GEMM kernel leaves both at zero when it exits.
+std::mutex g_counter_mutex;
+std::map<std::pair<int, hipStream_t>, int32_t*> g_counters;
+
+int counters_for(hipStream_t stream, int32_t** out) {
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return hip_error(err, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_counter_mutex);
+  auto key = std::make_pair(device, stream);
+  auto it = g_counters.find(key);
+  if (it != g_counters.end()) {
+    *out = it->second;
+    return MGG_OK;
+  }
+  int32_t* buf = nullptr;
+  err = hipMalloc(reinterpret_cast<void**>(&buf), 2 * sizeof(int32_t));
+  if (err != hipSuccess) return hip_error(err, "hipMalloc(dequeue counters)");
+  const int rc = launch_zero_i32(buf, 2, stream);
+  if (rc != MGG_OK) {
+    (void)hipFree(buf);
+    return rc;
+  }
+  g_counters.emplace(key, buf);
+  *out = buf;
+  return MGG_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+int set_error(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int hip_error(hipError_t err, const char* what) {
+  if (err == hipSuccess) return MGG_OK;
+  return set_error(MGG_ERR_HIP, std::string(what) + ": " + hipGetErrorString(err));
+}
+
+void clear_error() { g_last_error.clear(); }
+
+}  // namespace mgg
+
+using mgg::set_error;
+
+extern "C" {
+
+int mgg_abi_version(void) { return 1; }
+
+const char* mgg_last_error(void) { return mgg::g_last_error.c_str(); }
+
+int mgg_device_cu_count(int device, int* cu_count) {
+  mgg::clear_error();
+  if (cu_count == nullptr) return set_error(MGG_ERR_INVALID, "cu_count is null");
+  int n = 0;
+  const hipError_t err = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device);
+  if (err != hipSuccess) return mgg::hip_error(err, "hipDeviceGetAttribute(MultiprocessorCount)");
+  *cu_count = n;
+  return MGG_OK;
+}
+
+int mgg_expert_offsets_from_counts(const void* counts, int counts_type, int64_t num_experts,
+                                   void* offsets, int out_type, void* stream) {
+  mgg::clear_error();
+  if (num_experts < 0) return set_error(MGG_ERR_INVALID, "num_experts must be >= 0");
+  if (offsets == nullptr) return set_error(MGG_ERR_INVALID, "offsets is null");
+  if (num_experts > 0 && counts == nullptr) return set_error(MGG_ERR_INVALID, "counts is null");
+  return mgg::launch_offsets_from_counts(counts, counts_type, num_experts, offsets, out_type,
+                                         static_cast<hipStream_t>(stream));
+}
+
+int mgg_build_work_queue(const int32_t* expert_offsets, int64_t num_experts, int64_t n_size,
+                         int block_m, int block_n, int32_t* work_expert, int32_t* work_tile_m,
+                         int32_t* work_tile_n, int64_t num_work, void* stream) {
+  mgg::clear_error();
+  if (num_experts < 0 || num_experts > mgg::kMaxLdsExpertsQueue)
+    return set_error(MGG_ERR_UNSUPPORTED, "num_experts must be in [0, 8192]");
+  if (block_m <= 0 || block_n <= 0) return set_error(MGG_ERR_INVALID, "block sizes must be > 0");
+  if (n_size < 0) return set_error(MGG_ERR_INVALID, "n_size must be >= 0");
+  if (num_work < 0 || num_work >= (int64_t)1 << 31)
+    return set_error(MGG_ERR_INVALID, "num_work must be in [0, 2^31)");
+  if (num_work > 0 && (expert_offsets == nullptr || work_expert == nullptr ||
+                       work_tile_m == nullptr || work_tile_n == nullptr))
+    return set_error(MGG_ERR_INVALID, "null pointer with num_work > 0");
+  if (num_work > 0 && num_experts == 0)
+    return set_error(MGG_ERR_INVALID, "num_work > 0 with no experts");
+  return mgg::launch_build_work_queue(expert_offsets, (int32_t)num_experts, n_size, block_m,
+                                      block_n, work_expert, work_tile_m, work_tile_n,
+                                      (int32_t)num_work, static_cast<hipStream_t>(stream));
+}
+
+int mgg_expert_offsets_from_counts_host(const void* counts, int counts_type, int64_t num_experts,
+                                        void* offsets, int out_type) {
+  mgg::clear_error();
+  if (num_experts < 0) return set_error(MGG_ERR_INVALID, "num_experts must be >= 0");
+  if (offsets == nullptr) return set_error(MGG_ERR_INVALID, "offsets is null");
+  if (num_experts > 0 && counts == nullptr) return set_error(MGG_ERR_INVALID, "counts is null");
+  if ((counts_type != MGG_INT32 && counts_type != MGG_INT64) ||
+      (out_type != MGG_INT32 && out_type != MGG_INT64))
+    return set_error(MGG_ERR_INVALID, "counts_type and out_type must be MGG_INT32 or MGG_INT64");
+  // Same arithmetic as offsets_kernel: narrow each count to int32, sum in
+  // 64-bit two's complement, narrow the prefix to the output type.
+  uint64_t run = 0;
+  for (int64_t e = 0; e <= num_experts; ++e) {
+    if (e > 0) {
+      const int32_t c = counts_type == MGG_INT32
+                            ? static_cast<const int32_t*>(counts)[e - 1]
+                            : (int32_t) static_cast<const int64_t*>(counts)[e - 1];
+      run += (uint64_t)(int64_t)c;
+    }
+    if (out_type == MGG_INT32)
+      static_cast<int32_t*>(offsets)[e] = (int32_t)(int64_t)run;
+    else
+      static_cast<int64_t*>(offsets)[e] = (int64_t)run;
+  }
+  return MGG_OK;
+}
+
+int mgg_build_work_queue_host(const int64_t* expert_offsets, int64_t num_experts, int64_t n_size,
+                              int block_m, int block_n, int32_t* work_expert,
+                              int32_t* work_tile_m, int32_t* work_tile_n, int64_t num_work) {
+  mgg::clear_error();
+  if (num_experts < 0) return set_error(MGG_ERR_INVALID, "num_experts must be >= 0");
+  if (block_m <= 0 || block_n <= 0) return set_error(MGG_ERR_INVALID, "block sizes must be > 0");
+  if (n_size < 0) return set_error(MGG_ERR_INVALID, "n_size must be >= 0");
+  if (num_work < 0) return set_error(MGG_ERR_INVALID, "num_work must be >= 0");
+  if (num_work > 0 && (expert_offsets == nullptr || work_expert == nullptr ||
+                       work_tile_m == nullptr || work_tile_n == nullptr))
+    return set_error(MGG_ERR_INVALID, "null pointer with num_work > 0");
+  const int64_t n_tiles = (n_size + block_n - 1) / block_n;
+  int64_t w = 0;
+  for (int64_t e = 0; e < num_experts; ++e) {
+    const int64_t cnt = expert_offsets[e + 1] - expert_offsets[e];
+    const int64_t tm_count = cnt > 0 ? (cnt + block_m - 1) / block_m : 0;
+    for (int64_t tm = 0; tm < tm_count; ++tm) {
+      for (int64_t tn = 0; tn < n_tiles; ++tn, ++w) {
+        if (w >= num_work) return set_error(MGG_ERR_INVALID, "num_work smaller than the queue");
+        work_expert[w] = (int32_t)e;
+        work_tile_m[w] = (int32_t)tm;
+        work_tile_n[w] = (int32_t)tn;
+      }
+    }
+  }
+  if (w != num_work) return set_error(MGG_ERR_INVALID, "num_work larger than the queue");
+  return MGG_OK;
+}
+
+int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
+                     const int32_t* expert_offsets, int64_t m_size, int64_t k_size, int64_t n_size,
+                     int64_t num_experts, int64_t lda, int64_t ldb_e, int64_t ldb_k, int64_t ldc,
+                     const int32_t* work_expert, const int32_t* work_tile_m,
+                     const int32_t* work_tile_n, int64_t num_work, int block_m, int block_n,
+                     int num_workers, int use_atomic_queue, int32_t* work_counter, void* stream) {
+  mgg::clear_error();
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype != MGG_DTYPE_BF16 && dtype != MGG_DTYPE_FP16)
+    return set_error(MGG_ERR_UNSUPPORTED, "dtype must be MGG_DTYPE_BF16 or MGG_DTYPE_FP16");
+  const bool block_ok = (block_m == 64 || block_m == 128 || block_m == 256) &&
+                        (block_n == 64 || block_n == 128 || block_n == 256);
+  if (!block_ok)
+    return set_error(MGG_ERR_UNSUPPORTED, "block_m/block_n must each be one of 64, 128, 256");
+  if (m_size < 0 || k_size < 0 || n_size < 0 || num_experts < 0)
+    return set_error(MGG_ERR_INVALID, "sizes must be >= 0");
+  if (m_size == 0 || n_size == 0) return MGG_OK;  // C has no elements
+  if (k_size % 8 != 0 || n_size % 8 != 0)
+    return set_error(MGG_ERR_UNSUPPORTED, "K and N must be multiples of 8");
+  if (lda < k_size || ldb_k < n_size || ldc < n_size || ldb_e < 0)
+    return set_error(MGG_ERR_INVALID, "leading dimensions smaller than the matrix extents");
+  if (lda % 8 != 0 || ldb_k % 8 != 0 || ldb_e % 8 != 0 || ldc % 8 != 0)
+    return set_error(MGG_ERR_UNSUPPORTED, "strides must be multiples of 8 elements");
+  // A and B may be null only when nothing reads them (no experts or K == 0).
+  const bool reads_ab = num_experts > 0 && k_size > 0;
+  if (c == nullptr || expert_offsets == nullptr || (reads_ab && (a == nullptr || b == nullptr)))
+    return set_error(MGG_ERR_INVALID, "null operand pointer");
+  if (!mgg::aligned16(a) || !mgg::aligned16(b) || !mgg::aligned16(c))
+    return set_error(MGG_ERR_UNSUPPORTED, "operand base pointers must be 16-byte aligned");
+  // In-tile byte offsets are 32-bit: BM rows of A, K+8 rows of B.
+  const int64_t lim = ((int64_t)1 << 31) - 4096;
+  if ((int64_t)block_m * lda * 2 + k_size * 2 >= lim || (k_size + 8) * ldb_k * 2 >= lim)
+    return set_error(MGG_ERR_UNSUPPORTED, "row strides too large for 32-bit tile offsets");
+
+  int workers = num_workers;
+  if (workers <= 0) {
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return mgg::hip_error(err, "hipGetDevice");
+    err = hipDeviceGetAttribute(&workers, hipDeviceAttributeMultiprocessorCount, device);
+    if (err != hipSuccess) return mgg::hip_error(err, "hipDeviceGetAttribute");
+  }
+  if (workers > 65536) return set_error(MGG_ERR_INVALID, "num_workers must be <= 65536");
+
+  const int64_t n_tiles = (n_size + block_n - 1) / block_n;
+  if (num_work >= 0) {
+    if (num_work > 0 && (work_expert == nullptr || work_tile_m == nullptr || work_tile_n == nullptr))
+      return set_error(MGG_ERR_INVALID, "null work queue with num_work > 0");
+    if (num_work + workers >= ((int64_t)1 << 31))
+      return set_error(MGG_ERR_INVALID, "num_work + num_workers must be < 2^31");
+  } else {
+    if (num_experts > mgg::kMaxLdsExpertsGemm)
+      return set_error(MGG_ERR_UNSUPPORTED,
+                       "the device-derived queue supports at most 2048 experts; pass a "
+                       "prebuilt queue");
+    // Upper bound of the queue length for offsets inside [0, M].
+    const int64_t bound = (m_size / block_m + num_experts + 1) * n_tiles;
+    if (bound + workers >= ((int64_t)1 << 31))
+      return set_error(MGG_ERR_INVALID, "queue length may exceed 2^31");
+  }
+
+  mgg::GemmParams p{};
+  p.a = static_cast<const uint16_t*>(a);
+  p.b = static_cast<const uint16_t*>(b);
+  p.c = static_cast<uint16_t*>(c);
+  p.offsets = expert_offsets;
+  p.q_expert = num_work >= 0 ? work_expert : nullptr;
+  p.q_tile_m = num_work >= 0 ? work_tile_m : nullptr;
+  p.q_tile_n = num_work >= 0 ? work_tile_n : nullptr;
+  p.m = m_size;
+  p.k = k_size;
+  p.n = n_size;
+  p.lda = lda;
+  p.ldb_e = ldb_e;
+  p.ldb_k = ldb_k;
+  p.ldc = ldc;
+  p.num_experts = (int32_t)num_experts;
+  p.num_work = num_work >= 0 ? (int32_t)num_work : -1;
+  p.atomic = use_atomic_queue ? 1 : 0;
+  p.remap_xcd = 1;
+  if (p.atomic) {
+    int32_t* counters = nullptr;
+    const int rc = mgg::counters_for(st, &counters);
+    if (rc != MGG_OK) return rc;
+    p.counter = counters;
+    p.done = counters + 1;
+    p.report = work_counter;
+  }
+  return mgg::launch_grouped_gemm(dtype, block_m, block_n, p, workers, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,452 @@
+// Persistent expert-grouped GEMM for gfx950 (MI355X).
+//
+// One workgroup of 256 threads (4 wave64s) per CU walks a queue of
+// BLOCK_M x BLOCK_N output tiles (expert-major, then tile_m, then tile_n, the
+// order of src/triton_grouped_gemm.py:277-292).  Workers either stride over
+// the queue (the striped kernel, :101-154) or dequeue with a global atomic
+// (:157-233).  A tile is C[off_e + tm*BM + i, tn*BN + j] = sum_k
+// A[off_e + tm*BM + i, k] * B[e, k, tn*BN + j] (:36-98): rows past the expert's
+// count are never stored, fp32 accumulation, output rounded to the input type.
+//
+// Data path per 64-wide K stage:
+//   * A [BM x 64] moves HBM -> registers with 16-byte loads (8 lanes cover one
+//     128-byte row segment) and is written to LDS row-major, K contiguous.
+//   * B is stored [K, N] with N contiguous, but the MFMA wants 8 consecutive K
+//     per lane.  Each thread loads an 8(k) x 8(n) block with eight 16-byte
+//     loads (8 lanes cover 128 contiguous bytes of one row), transposes it in
+//     registers with 32 v_perm_b32, and writes eight 16-byte K-contiguous
+//     column segments: LDS holds B^T [BN x 64].
+//   * LDS rows hold 128 bytes at a 144-byte pitch, so 16 consecutive rows read
+//     at one chunk hit 16 distinct bank groups (no conflicts for the fragment
+//     reads or the stores) and every LDS address is a base plus an immediate.
+//   * Two LDS stages (2 x (BM + BN) x 144 B, 144 KiB at 256 x 256): the global
+//     loads of stage k+1 are in flight while stage k feeds the MFMAs; one
+//     barrier per stage.
+//   * Waves form a 2 x 2 grid; each owns a (BM/2) x (BN/2) sub-tile made of
+//     32 x 32 blocks computed with v_mfma_f32_32x32x16_{bf16,f16}.  The MFMA
+//     computes C^T = B^T A^T (B^T fragment as the first operand) so each lane
+//     ends up with 4 consecutive N values of one row per accumulator group,
+//     stored as one 8-byte write.
+#include "mgg.h"
+#include "mgg_internal.h"
+
+namespace mgg {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 256;
+constexpr int kBK = 64;                 // K elements per LDS stage
+constexpr int kLdsRow = kBK * 2 + 16;   // LDS row pitch: 8 chunks of 16 bytes + 16 pad
+
+struct Bf16 {
+  static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
+    bf16x2 v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+struct F16 {
+  static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
+    f16x2 v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+// Byte offset of 16-byte chunk `chunk` (0..7) of LDS row `row`.  The 144-byte
+// pitch (9 x 16 bytes, 9 odd) maps 16 consecutive rows at one chunk onto 16
+// distinct 16-byte bank groups, and keeps every address base + immediate.
+__device__ __forceinline__ int lds_off(int row, int chunk) { return row * kLdsRow + chunk * 16; }
+
+__device__ __forceinline__ u32x4 lds_load(const uint8_t* base, int off) {
+  return *reinterpret_cast<const u32x4*>(base + off);
+}
+__device__ __forceinline__ void lds_store(uint8_t* base, int off, u32x4 v) {
+  *reinterpret_cast<u32x4*>(base + off) = v;
+}
+// Raw (unswizzled, stride 0) buffer descriptor over `bytes` bytes at `base`;
+// word 3 is the gfx9-family default format.  Larger ranges are clamped to the
+// 32-bit record count: in-tile offsets are far below it.
+constexpr uint32_t kOutOfRange = 0x80000000u;  // any offset >= the record count
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int64_t cap = 0x7FFFFFF0LL;
+  const int32_t n = (int32_t)(bytes < 0 ? 0 : (bytes > cap ? cap : bytes));
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, int soff) {
+  return __builtin_bit_cast(u32x4,
+                            __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)voff, soff, 0));
+}
+
+// Per-expert tile prefix of the derived queue, built in LDS by the whole
+// workgroup: prefix[e] = sum_{j<e} ceil(max(off[j+1]-off[j],0)/BM) * n_tiles.
+// Returns the queue length W = prefix[E].  Same counts as
+// src/triton_grouped_gemm.py:253-271.
+template <int BM>
+__device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_prefix,
+                                 int32_t* s_scan) {
+  const int tid = threadIdx.x;
+  const int E = p.num_experts;
+  const int per = (E + kThreads - 1) / kThreads;
+  const int e0 = tid * per;
+  int32_t local = 0;
+  for (int i = 0; i < per; ++i) {
+    const int e = e0 + i;
+    if (e < E) {
+      const int64_t cnt = (int64_t)p.offsets[e + 1] - (int64_t)p.offsets[e];
+      const int64_t tiles = cnt > 0 ? ((cnt + BM - 1) / BM) * (int64_t)n_tiles : 0;
+      local += (int32_t)tiles;
+    }
+  }
+  s_scan[tid] = local;
+  __syncthreads();
+  // Hillis-Steele inclusive scan over the 256 per-thread sums.
+  for (int d = 1; d < kThreads; d <<= 1) {
+    const int32_t add = tid >= d ? s_scan[tid - d] : 0;
+    __syncthreads();
+    s_scan[tid] += add;
+    __syncthreads();
+  }
+  int32_t base = s_scan[tid] - local;
+  for (int i = 0; i < per; ++i) {
+    const int e = e0 + i;
+    if (e < E) {
+      s_prefix[e] = base;
+      const int64_t cnt = (int64_t)p.offsets[e + 1] - (int64_t)p.offsets[e];
+      base += cnt > 0 ? (int32_t)(((cnt + BM - 1) / BM) * (int64_t)n_tiles) : 0;
+    }
+  }
+  if (tid == kThreads - 1) s_prefix[E] = s_scan[kThreads - 1];
+  __syncthreads();
+  return s_prefix[E];
+}
+
+// Cooperative zero fill of C[M, N] (the empty-queue case, :369-371).
+__device__ void zero_fill(const GemmParams& p) {
+  const int64_t chunks_per_row = p.n / 8;
+  const int64_t total = p.m * chunks_per_row;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total; i += stride) {
+    const int64_t r = i / chunks_per_row;
+    const int64_t c8 = i - r * chunks_per_row;
+    *reinterpret_cast<u32x4*>(p.c + r * p.ldc + c8 * 8) = z;
+  }
+}
+
+// Computes one output tile.  All arguments are uniform across the workgroup,
+// so the early returns never split a barrier.
+template <int BM, int BN, class T>
+__device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int n_tiles,
+                                         const int32_t* s_prefix, uint8_t* lds_a,
+                                         uint8_t* lds_b) {
+  constexpr int kMB = BM / 64;                 // 32-row MFMA blocks per wave
+  constexpr int kNB = BN / 64;                 // 32-col MFMA blocks per wave
+  constexpr int kAChunks = BM * 8 / kThreads;  // 16-byte A chunks per thread per stage
+  constexpr int kARowsPerPass = kThreads / 8;  // A rows covered by one pass of the block
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave & 1;
+  const int wn = wave >> 1;
+
+  int e, tm, tn;
+  if (p.num_work >= 0) {
+    e = p.q_expert[item];
+    tm = p.q_tile_m[item];
+    tn = p.q_tile_n[item];
+    if ((uint32_t)e >= (uint32_t)p.num_experts || tm < 0 || (uint32_t)tn >= (uint32_t)n_tiles)
+      return;
+  } else {
+    int lo = 0, hi = p.num_experts - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_prefix[mid] <= item) lo = mid; else hi = mid - 1;
+    }
+    e = lo;
+    const int32_t local = item - s_prefix[e];
+    tm = local / n_tiles;
+    tn = local - tm * n_tiles;
+  }
+
+  const int64_t row0 = p.offsets[e];
+  const int64_t cnt = (int64_t)p.offsets[e + 1] - row0;
+  const int64_t m0 = (int64_t)tm * BM;
+  const int64_t left = cnt - m0;
+  if (left <= 0) return;
+  const int rows_valid = left < BM ? (int)left : BM;
+  const int64_t n0 = (int64_t)tn * BN;
+  const int64_t K = p.k;
+  const int64_t last_row = p.m - 1;
+
+  // ---- global sources: raw buffer descriptors (uniform, per tile) --------
+  // Each descriptor ends exactly at the last element of its operand, so a
+  // 16-byte load past it returns zeros: rows of A past M, rows of B past K
+  // and the B columns past N of the last row.  Rows of A inside [0, M) but
+  // past this expert's count load the next expert's data; their results are
+  // never stored.  Offsets stay 32-bit (the host bounds lda, ldb_k).
+  int64_t r0 = row0 + m0;
+  r0 = r0 < 0 ? 0 : (r0 > p.m ? p.m : r0);
+  const int64_t a_end = r0 < p.m ? ((p.m - 1 - r0) * p.lda + K) * 2 : 0;
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(p.a + r0 * p.lda, a_end);
+  const int64_t b_end = ((K - 1) * p.ldb_k + p.n - n0) * 2;
+  const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(p.b + (int64_t)e * p.ldb_e + n0, b_end);
+
+  const int a_kc = tid & 7;  // 16-byte chunk (8 K values) this thread loads
+  const uint32_t a_voff = (uint32_t)(((tid >> 3) * p.lda + a_kc * 8) * 2);
+  const uint32_t a_pass = (uint32_t)(kARowsPerPass * p.lda * 2);  // bytes between passes
+  const bool has_b = tid < BN;  // BN blocks of 8(k) x 8(n) per stage
+  const int b_kg = tid & 7;     // k group: rows 8*b_kg .. +7 of the stage
+  const int b_ng = tid >> 3;    // n group: columns 8*b_ng .. +7 of the tile
+  // Columns past N (edge tiles) are clamped onto column N-8: in bounds, and
+  // their results are never stored.
+  int64_t b_col = 8 * b_ng;
+  b_col = n0 + b_col > p.n - 8 ? p.n - 8 - n0 : b_col;
+  const uint32_t b_voff = has_b ? (uint32_t)((8 * b_kg * p.ldb_k + b_col) * 2) : kOutOfRange;
+  const uint32_t b_row = (uint32_t)(p.ldb_k * 2);
+
+  u32x4 a_reg[kAChunks];
+  u32x4 b_reg[8];
+
+  // A full stage (k0 + 64 <= K): every B row and every A column is in range,
+  // so the uniform stage offset rides in the SGPR offset; rows of A past M
+  // are out of range through their VGPR offset alone.
+  auto load_full = [&](int64_t k0) {
+    const int a_s = (int)(k0 * 2);
+#pragma unroll
+    for (int i = 0; i < kAChunks; ++i) a_reg[i] = bload(a_rsrc, a_voff + i * a_pass, a_s);
+    const int b_s = (int)((uint32_t)k0 * b_row);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) b_reg[s] = bload(b_rsrc, b_voff + s * b_row, b_s);
+  };
+  // The last, partial stage: the whole offset goes through the VGPR so the
+  // descriptor's range check zeroes A columns and B rows at k >= K.
+  auto load_tail = [&](int64_t k0) {
+    const bool a_in = k0 + a_kc * 8 < K;
+#pragma unroll
+    for (int i = 0; i < kAChunks; ++i)
+      a_reg[i] = bload(a_rsrc, a_in ? a_voff + (uint32_t)(k0 * 2) + i * a_pass : kOutOfRange, 0);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const bool b_in = has_b && k0 + 8 * b_kg + s < K;
+      b_reg[s] = bload(b_rsrc, b_in ? b_voff + ((uint32_t)k0 + s) * b_row : kOutOfRange, 0);
+    }
+  };
+
+  auto store_stage = [&](int buf) {
+    uint8_t* la = lds_a + buf * (BM * kLdsRow);
+    uint8_t* lb = lds_b + buf * (BN * kLdsRow);
+#pragma unroll
+    for (int i = 0; i < kAChunks; ++i)
+      lds_store(la, lds_off((tid >> 3) + kARowsPerPass * i, a_kc), a_reg[i]);
+    if (has_b) {
+      // 8x8 transpose of 16-bit values: b_reg[s].d[j] holds columns 2j, 2j+1
+      // of k row s; column t gets k rows 0..7 as four packed pairs.
+      u32x4 col[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t x = b_reg[2 * q][j];
+          const uint32_t y = b_reg[2 * q + 1][j];
+          col[2 * j][q] = __builtin_amdgcn_perm(y, x, 0x05040100u);
+          col[2 * j + 1][q] = __builtin_amdgcn_perm(y, x, 0x07060302u);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) lds_store(lb, lds_off(8 * b_ng + t, b_kg), col[t]);
+    }
+  };
+
+  f32x16 acc[kNB][kMB];
+#pragma unroll
+  for (int i = 0; i < kNB; ++i)
+#pragma unroll
+    for (int j = 0; j < kMB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int frag_row = lane & 31;
+  const int frag_half = lane >> 5;
+  const int a_row_base = wm * (BM / 2) + frag_row;
+  const int b_row_base = wn * (BN / 2) + frag_row;
+
+  auto compute_stage = [&](int buf) {
+    const uint8_t* la = lds_a + buf * (BM * kLdsRow);
+    const uint8_t* lb = lds_b + buf * (BN * kLdsRow);
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      const int chunk = 2 * kk + frag_half;
+      u32x4 af[kMB];
+      u32x4 bfr[kNB];
+#pragma unroll
+      for (int j = 0; j < kMB; ++j) af[j] = lds_load(la, lds_off(a_row_base + 32 * j, chunk));
+#pragma unroll
+      for (int i = 0; i < kNB; ++i) bfr[i] = lds_load(lb, lds_off(b_row_base + 32 * i, chunk));
+#pragma unroll
+      for (int i = 0; i < kNB; ++i)
+#pragma unroll
+        for (int j = 0; j < kMB; ++j) acc[i][j] = T::mfma(bfr[i], af[j], acc[i][j]);
+      // Keep the next sub-step's fragment loads from being hoisted above
+      // these MFMAs (bounds the live fragment registers to two sub-steps).
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  const int nk = (int)((K + kBK - 1) / kBK);
+  const int nk_full = (int)(K / kBK);  // stages with k0 + 64 <= K
+  if (nk_full > 0) load_full(0); else load_tail(0);
+  store_stage(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      if (kt + 1 < nk_full) load_full((int64_t)(kt + 1) * kBK);
+      else load_tail((int64_t)(kt + 1) * kBK);
+    }
+    compute_stage(buf);
+    if (more) store_stage(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: acc[i][j] register r holds D[n][m] of the 32x32 block with
+  // n = 8*(r/4) + 4*(lane/32) + r%4, m = lane%32 (D = C^T).
+  const int64_t c_row_base = row0 + m0;
+#pragma unroll
+  for (int j = 0; j < kMB; ++j) {
+    const int m = wm * (BM / 2) + 32 * j + frag_row;
+    const int64_t grow = c_row_base + m;
+    const bool row_ok = m < rows_valid && grow >= 0 && grow <= last_row;
+    uint16_t* crow = p.c + grow * p.ldc;
+#pragma unroll
+    for (int i = 0; i < kNB; ++i) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t n = n0 + wn * (BN / 2) + 32 * i + 8 * g + 4 * frag_half;
+        if (row_ok && n < p.n) {
+          u32x2 v;
+          v[0] = T::pack(acc[i][j][4 * g + 0], acc[i][j][4 * g + 1]);
+          v[1] = T::pack(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+          *reinterpret_cast<u32x2*>(crow + n) = v;
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int BN, class T>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(1, 1))) void
+grouped_gemm_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds_a[2 * BM * kLdsRow];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_b[2 * BN * kLdsRow];
+  __shared__ int32_t s_prefix[kMaxLdsExpertsGemm + 1];
+  __shared__ int32_t s_scan[kThreads];
+  __shared__ int32_t s_item;
+
+  const int tid = threadIdx.x;
+  const int G = gridDim.x;
+  const int n_tiles = (int)((p.n + BN - 1) / BN);
+
+  const int32_t W = p.num_work >= 0 ? p.num_work : derive_prefix<BM>(p, n_tiles, s_prefix, s_scan);
+  if (W == 0) {
+    zero_fill(p);
+    return;
+  }
+
+  // XCD-aware worker numbering: workgroup b runs on XCD b % 8, so giving the
+  // 8 XCDs contiguous worker ranges makes each round's consecutive queue
+  // items (same expert, same tile_m) share one XCD's L2.
+  int v = blockIdx.x;
+  if (p.remap_xcd && (G & 7) == 0) v = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+
+  // Striped: items v, v+G, v+2G, ...  Atomic: the leader thread takes the
+  // next ticket from the global counter and broadcasts it through LDS.
+  auto next_ticket = [&]() -> int32_t {
+    if (tid == 0) s_item = atomicAdd(p.counter, 1);
+    __syncthreads();
+    const int32_t t = s_item;
+    __syncthreads();
+    return t;
+  };
+  int32_t w = p.atomic ? next_ticket() : v;
+  while ((uint32_t)w < (uint32_t)W) {
+    run_tile<BM, BN, T>(p, w, n_tiles, s_prefix, lds_a, lds_b);
+    w = p.atomic ? next_ticket() : w + G;
+  }
+  if (!p.atomic) return;
+  // Every worker has fetched its final (out-of-range) ticket before adding to
+  // `done`, so the last one to arrive reads the final count (W + G when no
+  // worker stops early), hands it to the caller's work_counter and returns
+  // both library counters to zero for the next launch on this stream.
+  if (tid == 0) {
+    if (atomicAdd(p.done, 1) == G - 1) {
+      const int32_t final_count = atomicExch(p.counter, 0);
+      atomicExch(p.done, 0);
+      if (p.report != nullptr) atomicExch(p.report, final_count);
+    }
+  }
+}
+
+__global__ void zero_i32_kernel(int32_t* ptr, int count) {
+  for (int i = threadIdx.x; i < count; i += blockDim.x) ptr[i] = 0;
+}
+
+template <class T>
+int launch_typed(int block_m, int block_n, const GemmParams& p, int workers, hipStream_t stream) {
+#define MGG_CASE(BM_, BN_)                                                                  \
+  if (block_m == BM_ && block_n == BN_) {                                                  \
+    hipLaunchKernelGGL((grouped_gemm_kernel<BM_, BN_, T>), dim3(workers), dim3(kThreads), 0, \
+                       stream, p);                                                         \
+    return MGG_OK;                                                                          \
+  }
+  MGG_CASE(256, 256)
+  MGG_CASE(256, 128)
+  MGG_CASE(128, 256)
+  MGG_CASE(128, 128)
+  MGG_CASE(128, 64)
+  MGG_CASE(64, 128)
+  MGG_CASE(64, 64)
+  MGG_CASE(256, 64)
+  MGG_CASE(64, 256)
+#undef MGG_CASE
+  return set_error(MGG_ERR_UNSUPPORTED, "block_m/block_n must each be one of 64, 128, 256");
+}
+
+}  // namespace
+
+int launch_grouped_gemm(int dtype, int block_m, int block_n, const GemmParams& p, int workers,
+                        hipStream_t stream) {
+  int rc;
+  if (dtype == MGG_DTYPE_BF16)
+    rc = launch_typed<Bf16>(block_m, block_n, p, workers, stream);
+  else if (dtype == MGG_DTYPE_FP16)
+    rc = launch_typed<F16>(block_m, block_n, p, workers, stream);
+  else
+    return set_error(MGG_ERR_UNSUPPORTED, "dtype must be MGG_DTYPE_BF16 or MGG_DTYPE_FP16");
+  if (rc != MGG_OK) return rc;
+  return hip_error(hipGetLastError(), "grouped_gemm_kernel launch");
+}
+
+int launch_zero_i32(int32_t* ptr, int count, hipStream_t stream) {
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, stream, ptr, count);
+  return hip_error(hipGetLastError(), "zero_i32_kernel launch");
+}
+
+}  // namespace mgg

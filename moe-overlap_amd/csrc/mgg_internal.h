@@ -1,0 +1,62 @@
+// Internal declarations shared by the libmgg HIP sources (not part of the C ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace mgg {
+
+// Records `msg` as the calling thread's last error and returns `code`.
+int set_error(int code, const std::string& msg);
+// Maps a failed HIP call to MGG_ERR_HIP with the runtime's message.
+int hip_error(hipError_t err, const char* what);
+void clear_error();
+
+// Largest expert count whose per-expert tile prefix fits in LDS.
+constexpr int kMaxLdsExpertsGemm = 2048;
+constexpr int kMaxLdsExpertsQueue = 8192;
+
+// Launch arguments of the grouped-GEMM kernels.  Element strides; byte
+// pointers so one struct serves every element type.
+struct GemmParams {
+  const uint16_t* a;
+  const uint16_t* b;
+  uint16_t* c;
+  const int32_t* offsets;
+  const int32_t* q_expert;  // prebuilt queue (num_work >= 0) or null
+  const int32_t* q_tile_m;
+  const int32_t* q_tile_n;
+  int32_t* counter;  // atomic mode: library-owned dequeue counter (zero on entry)
+  int32_t* done;     // atomic mode: library-owned exit counter (zero on entry)
+  int32_t* report;   // atomic mode: caller's work_counter, receives the final count, or null
+  int64_t m;
+  int64_t k;
+  int64_t n;
+  int64_t lda;
+  int64_t ldb_e;
+  int64_t ldb_k;
+  int64_t ldc;
+  int32_t num_experts;
+  int32_t num_work;  // < 0: derive the queue from the offsets on the device
+  int32_t atomic;
+  int32_t remap_xcd;
+};
+
+// Launches the grouped GEMM for one (dtype, block_m, block_n) on `stream`
+// with `workers` workgroups.  Returns MGG_OK or an error code.
+int launch_grouped_gemm(int dtype, int block_m, int block_n, const GemmParams& p, int workers,
+                        hipStream_t stream);
+
+// Zeroes `count` int32 values with a fill kernel on `stream`.
+int launch_zero_i32(int32_t* ptr, int count, hipStream_t stream);
+
+int launch_offsets_from_counts(const void* counts, int counts_type, int64_t num_experts,
+                               void* offsets, int out_type, hipStream_t stream);
+
+int launch_build_work_queue(const int32_t* offsets, int32_t num_experts, int64_t n_size,
+                            int block_m, int block_n, int32_t* we, int32_t* wm, int32_t* wn,
+                            int32_t num_work, hipStream_t stream);
+
+}  // namespace mgg

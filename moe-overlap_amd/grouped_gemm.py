@@ -1,0 +1,328 @@
+"""Expert-grouped GEMM for MoE on MI355X (gfx950): the host side of the drop-in.
+
+Module-level API of the reference's ``src/triton_grouped_gemm.py``, same names,
+arguments, results and ``ValueError`` conditions, computed by hand-written HIP
+kernels in libmgg.so (``include/mgg.h``) instead of Triton:
+
+* ``persistent_grouped_gemm``          (reference :326-443)
+* ``expert_offsets_from_recv_counts``  (reference :300-323)
+* ``_build_work_queue``                (reference :240-297, with its FIFO cache)
+* ``reference_grouped_gemm``           (reference :446-457, the per-expert loop)
+
+Differences, all in arguments that do not change results:
+
+* ``num_sms`` defaults to the device's CU count (256 on MI355X) instead of 24;
+  an explicit value is honoured (it doubles as a CU-reservation knob).
+* ``block_m``/``block_n`` default to ``None``: 256 x 256 tiles (128 x 256 when
+  the average expert holds fewer than 256 rows).  Explicit values must be 64,
+  128 or 256; they set the tile and queue granularity exactly as before.
+* ``block_k``, ``num_warps``, ``num_stages`` are accepted and ignored: the
+  kernel's K stage (64), wave count (4) and LDS double buffering are fixed by
+  its design.
+* ``queue="device"`` (default) derives the same (expert, tile_m, tile_n) queue
+  inside the kernel from the offsets, so a call never waits on the device;
+  ``queue="prebuilt"`` goes through ``_build_work_queue`` (a host round trip
+  for the cache key, as in the reference).  Outputs are identical.
+* ``work_counter`` (atomic mode) receives the final dequeue count W + G, the
+  value the reference leaves there, while the dequeue itself runs on a
+  library-owned per-stream counter, so no separate zeroing launch is needed.
+* Operands whose inner stride is not 1, whose rows are not 16-byte aligned, or
+  with K or N not a multiple of 8, are copied (and zero-padded) on the device
+  first.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Tuple, Union
+
+import numpy as np
+import torch
+
+import mgg_native as _nat
+
+__all__ = [
+    "persistent_grouped_gemm",
+    "expert_offsets_from_recv_counts",
+    "reference_grouped_gemm",
+    "_build_work_queue",
+    "grouped_gemm_flops",
+]
+
+_SUPPORTED_BLOCKS = (64, 128, 256)
+_DTYPE_CODES = {torch.bfloat16: _nat.MGG_DTYPE_BF16, torch.float16: _nat.MGG_DTYPE_FP16}
+
+_WORK_QUEUE_CACHE: dict = {}
+_WORK_QUEUE_CACHE_MAX = 32
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+# --------------------------------------------------------------------------
+# expert offsets
+# --------------------------------------------------------------------------
+def expert_offsets_from_recv_counts(
+    num_recv_tokens_per_expert: Union[torch.Tensor, List[int]],
+    device: Optional[torch.device] = None,
+    dtype: torch.dtype = torch.int32,
+) -> torch.Tensor:
+    """``[0, c_0, c_0 + c_1, ...]`` of length E+1 from per-expert counts.
+
+    Reference: src/triton_grouped_gemm.py:300-323.  A list becomes an int32
+    tensor; a tensor is narrowed to int32 and flattened; ``device`` moves it;
+    the prefix sum is taken in int64 and cast to ``dtype`` (so int32 sums wrap).
+    The scan runs in libmgg (device kernel for GPU tensors, host loop for CPU
+    tensors).
+    """
+    if isinstance(num_recv_tokens_per_expert, list):
+        t = torch.tensor(num_recv_tokens_per_expert, dtype=torch.int32)
+    else:
+        t = num_recv_tokens_per_expert.flatten()
+        if t.dtype not in (torch.int32, torch.int64):
+            t = t.to(torch.int32)
+    if device is not None:
+        t = t.to(device)
+    t = t.contiguous()
+    num = t.numel()
+    out_dtype = dtype if dtype in (torch.int32, torch.int64) else torch.int64
+    out = torch.empty(num + 1, dtype=out_dtype, device=t.device)
+    in_code = _nat.MGG_INT32 if t.dtype == torch.int32 else _nat.MGG_INT64
+    out_code = _nat.MGG_INT32 if out_dtype == torch.int32 else _nat.MGG_INT64
+    lib = _nat.lib()
+    if t.device.type == "cuda":
+        with torch.cuda.device(t.device):
+            _nat.check(
+                lib.mgg_expert_offsets_from_counts(
+                    _ptr(t), in_code, num, _ptr(out), out_code, _stream_handle(t.device)
+                )
+            )
+    elif t.device.type == "cpu":
+        _nat.check(lib.mgg_expert_offsets_from_counts_host(_ptr(t), in_code, num, _ptr(out), out_code))
+    else:
+        raise ValueError(f"unsupported device {t.device}")
+    return out if out_dtype == dtype else out.to(dtype)
+
+
+# --------------------------------------------------------------------------
+# work queue
+# --------------------------------------------------------------------------
+def _queue_length(offsets_host: np.ndarray, n_size: int, block_m: int, block_n: int) -> int:
+    counts = np.clip(offsets_host[1:] - offsets_host[:-1], 0, None)
+    tiles_m = (counts + block_m - 1) // block_m
+    tiles_n = (int(n_size) + block_n - 1) // block_n
+    return int(tiles_m.sum()) * tiles_n
+
+
+def _build_work_queue(
+    expert_offsets: torch.Tensor,
+    n_size: int,
+    block_m: int,
+    block_n: int,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(expert_id, tile_m, tile_n) int32 vectors, expert-major then tile_m then tile_n.
+
+    Reference: src/triton_grouped_gemm.py:240-297.  Cached by (offsets bytes,
+    n_size, block_m, block_n) with FIFO eviction at 32 entries; the offsets
+    are copied to the host for the key (a device sync, as in the reference).
+    Built by libmgg on the offsets' device.
+    """
+    assert expert_offsets.dim() == 1
+    if block_m <= 0 or block_n <= 0:
+        raise ValueError("block_m and block_n must be positive.")
+    device = expert_offsets.device
+    host = expert_offsets.detach().to("cpu", torch.int64).contiguous().numpy()
+    key = (host.tobytes(), int(n_size), int(block_m), int(block_n))
+    cached = _WORK_QUEUE_CACHE.get(key)
+    if cached is not None and cached[0].device == device:
+        return cached
+
+    num_experts = host.shape[0] - 1
+    total = _queue_length(host, n_size, block_m, block_n) if num_experts > 0 else 0
+    we = torch.empty(total, dtype=torch.int32, device=device)
+    wm = torch.empty(total, dtype=torch.int32, device=device)
+    wn = torch.empty(total, dtype=torch.int32, device=device)
+    lib = _nat.lib()
+    if total > 0:
+        if device.type == "cuda":
+            off32 = expert_offsets.to(torch.int32).contiguous()
+            with torch.cuda.device(device):
+                _nat.check(
+                    lib.mgg_build_work_queue(
+                        _ptr(off32), num_experts, int(n_size), int(block_m), int(block_n),
+                        _ptr(we), _ptr(wm), _ptr(wn), total, _stream_handle(device),
+                    )
+                )
+        else:
+            _nat.check(
+                lib.mgg_build_work_queue_host(
+                    host.ctypes.data_as(ctypes.c_void_p), num_experts, int(n_size),
+                    int(block_m), int(block_n), _ptr(we), _ptr(wm), _ptr(wn), total,
+                )
+            )
+    result = (we, wm, wn)
+    if len(_WORK_QUEUE_CACHE) >= _WORK_QUEUE_CACHE_MAX:
+        _WORK_QUEUE_CACHE.pop(next(iter(_WORK_QUEUE_CACHE)))
+    _WORK_QUEUE_CACHE[key] = result
+    return result
+
+
+# --------------------------------------------------------------------------
+# grouped GEMM
+# --------------------------------------------------------------------------
+def _default_blocks(m_total: int, num_experts: int) -> Tuple[int, int]:
+    if num_experts > 0 and m_total // num_experts < 256:
+        return 128, 256
+    return 256, 256
+
+
+def _fast_layout(t: torch.Tensor) -> bool:
+    """Unit inner stride, 16-byte aligned base, outer strides multiples of 8."""
+    if t.stride(-1) != 1 or t.data_ptr() % 16 != 0:
+        return False
+    return all(t.stride(d) % 8 == 0 for d in range(t.dim() - 1) if t.size(d) > 1)
+
+
+def _gemm_operand(t: torch.Tensor) -> torch.Tensor:
+    """`t` itself when the kernel can read it in place, else a device copy."""
+    if _fast_layout(t):
+        return t
+    t = t.contiguous()
+    if not _fast_layout(t):
+        t = t.clone(memory_format=torch.contiguous_format)
+    return t
+
+
+def persistent_grouped_gemm(
+    a_cat: torch.Tensor,
+    b_expert: torch.Tensor,
+    expert_offsets: torch.Tensor,
+    num_sms: Optional[int] = None,
+    block_m: Optional[int] = None,
+    block_n: Optional[int] = None,
+    block_k: int = 32,
+    use_atomic_queue: bool = True,
+    work_counter: Optional[torch.Tensor] = None,
+    num_warps: int = 8,
+    num_stages: int = 3,
+    *,
+    queue: str = "device",
+) -> torch.Tensor:
+    """C[s_e:t_e] = A[s_e:t_e] @ B[e] for every expert, persistent workers.
+
+    Reference: src/triton_grouped_gemm.py:326-443.  a_cat [M, K], b_expert
+    [E, K, N], expert_offsets [E+1]; bf16 or fp16; fp32 accumulation; output
+    [M, N] in the input dtype (rows outside every expert range are left
+    uninitialised; an empty queue zero-fills).  Launches asynchronously on the
+    current stream of a_cat's device.
+    """
+    if a_cat.device.type != "cuda" or b_expert.device.type != "cuda":
+        raise ValueError("persistent_grouped_gemm requires CUDA tensors.")
+    if a_cat.dim() != 2 or b_expert.dim() != 3:
+        raise ValueError("Shapes must be a_cat [M, K], b_expert [E, K, N].")
+    if a_cat.size(1) != b_expert.size(1):
+        raise ValueError("K dimension mismatch between a_cat and b_expert.")
+    if expert_offsets.numel() != b_expert.size(0) + 1:
+        raise ValueError("expert_offsets must have shape [num_experts + 1].")
+    if expert_offsets.device != a_cat.device:
+        raise ValueError("expert_offsets must be on the same device as input tensors.")
+    if a_cat.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("a_cat dtype must be bf16/fp16.")
+    if b_expert.dtype != a_cat.dtype:
+        raise ValueError("b_expert dtype should match a_cat dtype.")
+    if queue not in ("device", "prebuilt"):
+        raise ValueError("queue must be 'device' or 'prebuilt'.")
+
+    m_total, k_size = a_cat.shape
+    num_experts, _, n_size = b_expert.shape
+    if block_m is None or block_n is None:
+        dm, dn = _default_blocks(m_total, num_experts)
+        block_m = dm if block_m is None else block_m
+        block_n = dn if block_n is None else block_n
+    if block_m not in _SUPPORTED_BLOCKS or block_n not in _SUPPORTED_BLOCKS:
+        raise ValueError("block_m and block_n must each be one of 64, 128, 256.")
+    device = a_cat.device
+    if num_sms is None:
+        num_sms = _nat.device_cu_count(device.index if device.index is not None else torch.cuda.current_device())
+    if int(num_sms) <= 0:
+        raise ValueError("num_sms must be positive.")
+
+    counter_dev = None
+    if use_atomic_queue and work_counter is not None:
+        if work_counter.numel() != 1 or work_counter.dtype != torch.int32:
+            raise ValueError("work_counter must be int32 tensor of shape [1].")
+        counter_dev = work_counter.to(device)
+        if not counter_dev.is_contiguous():
+            counter_dev = counter_dev.contiguous()
+
+    # K or N not a multiple of 8: zero-pad on the device (zeros add nothing).
+    k_pad = (k_size + 7) // 8 * 8
+    n_pad = (n_size + 7) // 8 * 8
+    a_op, b_op = a_cat, b_expert
+    if k_pad != k_size:
+        a_op = torch.nn.functional.pad(a_op, (0, k_pad - k_size))
+        b_op = torch.nn.functional.pad(b_op, (0, 0, 0, k_pad - k_size))
+    if n_pad != n_size:
+        b_op = torch.nn.functional.pad(b_op, (0, n_pad - n_size))
+    a_op = _gemm_operand(a_op)
+    b_op = _gemm_operand(b_op)
+    # Leading dimensions; a size-1 dimension's stride is never used.
+    lda = a_op.stride(0) if m_total > 1 else k_pad
+    ldb_k = b_op.stride(1) if k_pad > 1 else n_pad
+    ldb_e = b_op.stride(0) if num_experts > 1 else k_pad * ldb_k
+    c_op = torch.empty((m_total, n_pad), device=device, dtype=a_cat.dtype)
+
+    if queue == "prebuilt":
+        we, wm, wn = _build_work_queue(expert_offsets, n_size=n_size, block_m=block_m, block_n=block_n)
+        num_work = we.numel()
+    else:
+        we = wm = wn = None
+        num_work = -1
+    off32 = expert_offsets if expert_offsets.dtype == torch.int32 else expert_offsets.to(torch.int32)
+    off32 = off32.contiguous()
+
+    lib = _nat.lib()
+    with torch.cuda.device(device):
+        _nat.check(
+            lib.mgg_grouped_gemm(
+                _DTYPE_CODES[a_cat.dtype], _ptr(a_op), _ptr(b_op), _ptr(c_op),
+                _ptr(off32), m_total, k_pad, n_pad,
+                num_experts, lda, ldb_e, ldb_k, c_op.stride(0),
+                _ptr(we), _ptr(wm), _ptr(wn), num_work,
+                int(block_m), int(block_n), int(num_sms), 1 if use_atomic_queue else 0,
+                _ptr(counter_dev), _stream_handle(device),
+            )
+        )
+    if n_pad != n_size:
+        return c_op[:, :n_size].contiguous()
+    return c_op
+
+
+def reference_grouped_gemm(
+    a_cat: torch.Tensor, b_expert: torch.Tensor, expert_offsets: torch.Tensor
+) -> torch.Tensor:
+    """Per-expert torch matmul loop (src/triton_grouped_gemm.py:446-457).
+
+    The comparison loop of the reference API: one ``a[s:t] @ b[e]`` per
+    non-empty expert on the tensors' own device (hipBLASLt on a GPU), rows
+    outside every expert range uninitialised.  Not used by the kernels.
+    """
+    out = torch.empty((a_cat.size(0), b_expert.size(2)), device=a_cat.device, dtype=a_cat.dtype)
+    offs = expert_offsets.detach().to("cpu", torch.int64).tolist()
+    for e in range(b_expert.size(0)):
+        s, t = offs[e], offs[e + 1]
+        if t <= s:
+            continue
+        out[s:t] = a_cat[s:t] @ b_expert[e]
+    return out
+
+
+def grouped_gemm_flops(expert_offsets, k_size: int, n_size: int) -> int:
+    """Algorithmic FLOPs 2 * sum_e max(c_e, 0) * K * N (masked work not counted)."""
+    offs = torch.as_tensor(expert_offsets).detach().to("cpu", torch.int64)
+    counts = (offs[1:] - offs[:-1]).clamp_min(0)
+    return 2 * int(counts.sum()) * int(k_size) * int(n_size)

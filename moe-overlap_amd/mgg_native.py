@@ -1,0 +1,99 @@
+"""ctypes binding of libmgg.so, the gfx950 C-ABI library (include/mgg.h).
+
+The library is built in-tree by ``build_native.build()``.  It is loaded after
+``import torch`` so that it binds to the HIP runtime torch already loaded
+(same soname), and therefore shares torch's devices and streams.  A missing
+library raises: there is no other implementation of these entry points.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch  # noqa: F401  (loads the HIP runtime this library must share)
+
+LIB_PATH = Path(__file__).resolve().parent / "libmgg.so"
+ABI_VERSION = 1
+
+MGG_OK = 0
+MGG_ERR_INVALID = 1
+MGG_ERR_UNSUPPORTED = 2
+MGG_ERR_HIP = 3
+
+MGG_DTYPE_BF16 = 0
+MGG_DTYPE_FP16 = 1
+MGG_INT32 = 0
+MGG_INT64 = 1
+
+_c_i32 = ctypes.c_int
+_c_i64 = ctypes.c_int64
+_c_ptr = ctypes.c_void_p
+
+# name -> argument types (all return int except mgg_last_error)
+_SIGNATURES = {
+    "mgg_abi_version": [],
+    "mgg_device_cu_count": [_c_i32, ctypes.POINTER(_c_i32)],
+    "mgg_expert_offsets_from_counts": [_c_ptr, _c_i32, _c_i64, _c_ptr, _c_i32, _c_ptr],
+    "mgg_expert_offsets_from_counts_host": [_c_ptr, _c_i32, _c_i64, _c_ptr, _c_i32],
+    "mgg_build_work_queue": [
+        _c_ptr, _c_i64, _c_i64, _c_i32, _c_i32, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr,
+    ],
+    "mgg_build_work_queue_host": [
+        _c_ptr, _c_i64, _c_i64, _c_i32, _c_i32, _c_ptr, _c_ptr, _c_ptr, _c_i64,
+    ],
+    "mgg_grouped_gemm": [
+        _c_i32, _c_ptr, _c_ptr, _c_ptr,  # dtype, a, b, c
+        _c_ptr, _c_i64, _c_i64, _c_i64,  # offsets, M, K, N
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,  # E, lda, ldb_e, ldb_k, ldc
+        _c_ptr, _c_ptr, _c_ptr, _c_i64,  # queue, num_work
+        _c_i32, _c_i32, _c_i32, _c_i32,  # block_m, block_n, num_workers, atomic
+        _c_ptr, _c_ptr,  # work_counter, stream
+    ],
+}
+EXPORTED = tuple(_SIGNATURES) + ("mgg_last_error",)
+
+_lib = None
+
+
+class NativeError(RuntimeError):
+    """A libmgg entry point returned an error status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"libmgg error {code}: {message}")
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libmgg.so once; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
+            "g.build()'` (or moe-overlap_amd/build_native.py)"
+        )
+    handle = ctypes.CDLL(str(LIB_PATH))
+    for name, argtypes in _SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.argtypes = argtypes
+        fn.restype = _c_i32
+    handle.mgg_last_error.argtypes = []
+    handle.mgg_last_error.restype = ctypes.c_char_p
+    version = handle.mgg_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"libmgg ABI version {version}, expected {ABI_VERSION}: rebuild it")
+    _lib = handle
+    return _lib
+
+
+def check(code: int) -> None:
+    """Raises NativeError with the library's message for a non-zero status."""
+    if code != MGG_OK:
+        raise NativeError(code, lib().mgg_last_error().decode(errors="replace"))
+
+
+def device_cu_count(device_index: int) -> int:
+    n = _c_i32(0)
+    check(lib().mgg_device_cu_count(int(device_index), ctypes.byref(n)))
+    return int(n.value)

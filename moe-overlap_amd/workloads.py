@@ -1,0 +1,100 @@
+"""Synthetic routed-token workloads of the BASELINE configs (fixed seeds).
+
+Counts come from the routing recipes; tensors are N(0,1) activations and
+N(0, 1/K) expert weights.  Tensors are drawn with a torch Generator seeded on
+the target device (so a GPU run does not generate hundreds of MB on the host);
+the same seed on the same device type gives the same tensors.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+import torch
+
+# Per-expert counts of the skewed-routing config at its pinned recipe
+# (8192 tokens, top-2 over 16 experts, logits N(0,1) with torch seed 0 plus a
+# per-expert bias ln(Zipf(1.2)) drawn with numpy default_rng(0)).
+SKEWED_COUNTS = (0, 0, 586, 3269, 7, 4331, 0, 0, 0, 0, 0, 0, 0, 8191, 0, 0)
+
+
+@dataclass
+class GroupedGemmCase:
+    name: str
+    counts: torch.Tensor  # int32 [E] (CPU)
+    k: int
+    n: int
+    a: Optional[torch.Tensor] = None  # [M, K]
+    b: Optional[torch.Tensor] = None  # [E, K, N]
+
+    @property
+    def num_experts(self) -> int:
+        return int(self.counts.numel())
+
+    @property
+    def m(self) -> int:
+        return int(self.counts.sum())
+
+    @property
+    def flops(self) -> int:
+        return 2 * self.m * self.k * self.n
+
+    def algorithmic_bytes(self, elem_size: int = 2) -> int:
+        """A read once, B of every non-empty expert read once, C written once."""
+        nonempty = int((self.counts > 0).sum())
+        return (self.m * self.k + nonempty * self.k * self.n + self.m * self.n) * elem_size
+
+
+def skewed_counts_from_recipe(tokens: int = 8192, experts: int = 16, top_k: int = 2) -> torch.Tensor:
+    """Routing counts of the skewed config, recomputed from its recipe."""
+    gen = torch.Generator().manual_seed(0)
+    logits = torch.randn(tokens, experts, generator=gen)
+    zipf = np.random.default_rng(0).zipf(1.2, experts)
+    bias = torch.from_numpy(np.log(zipf.astype(np.float64))).float()
+    idx = torch.topk(logits + bias, top_k, dim=1).indices
+    return torch.bincount(idx.flatten(), minlength=experts).to(torch.int32)
+
+
+def topk_counts(tokens: int, experts: int, top_k: int, softmax: bool = False) -> torch.Tensor:
+    """Counts of top-k routing on N(0,1) logits (torch seed 0)."""
+    gen = torch.Generator().manual_seed(0)
+    logits = torch.randn(tokens, experts, generator=gen)
+    if softmax:
+        logits = torch.softmax(logits, dim=-1)
+    idx = torch.topk(logits, top_k, dim=1).indices
+    return torch.bincount(idx.flatten(), minlength=experts).to(torch.int32)
+
+
+def make_case(
+    name: str,
+    device: Optional[torch.device] = None,
+    dtype: torch.dtype = torch.bfloat16,
+    seed: int = 0,
+    materialize: bool = True,
+) -> GroupedGemmCase:
+    """One of: cpu_plumbing (cfg 1), uniform (cfg 2), skewed (cfg 3)."""
+    if name == "cpu_plumbing":
+        case = GroupedGemmCase(name, torch.full((8,), 128, dtype=torch.int32), 512, 1024)
+    elif name == "uniform":
+        case = GroupedGemmCase(name, torch.full((16,), 512, dtype=torch.int32), 2048, 4096)
+    elif name == "skewed":
+        case = GroupedGemmCase(name, torch.tensor(SKEWED_COUNTS, dtype=torch.int32), 2048, 4096)
+    else:
+        raise ValueError(f"unknown workload {name!r}")
+    if materialize:
+        fill_operands(case, device=device, dtype=dtype, seed=seed)
+    return case
+
+
+def fill_operands(case: GroupedGemmCase, device=None, dtype=torch.bfloat16, seed: int = 0) -> None:
+    """a ~ N(0,1) [M, K], b ~ N(0, 1/K) [E, K, N], drawn in fp32 then cast."""
+    device = torch.device("cpu") if device is None else torch.device(device)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    a = torch.randn(case.m, case.k, generator=gen, device=device, dtype=torch.float32)
+    b = torch.randn(case.num_experts, case.k, case.n, generator=gen, device=device,
+                    dtype=torch.float32)
+    b.mul_(1.0 / math.sqrt(case.k))
+    case.a = a.to(dtype)
+    case.b = b.to(dtype)

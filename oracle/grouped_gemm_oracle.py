@@ -1,0 +1,147 @@
+"""CPU oracle for the expert-grouped GEMM path -- TEST INFRASTRUCTURE ONLY.
+
+A restatement, in numpy, of the reference's algorithm for this path
+(Hongyu15/moe-overlap, ``src/triton_grouped_gemm.py``), used as the checker in
+``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py``.  Nothing in the product (``moe-overlap_amd/``) imports it.
+
+Functions and what pins each one (tests/test_oracle_*.py):
+
+* ``expert_offsets_from_recv_counts`` -- reference :300-323.  Pinned by the
+  closed form [0, cumsum], hand-computed cases, the wrap of int32 sums and
+  the committed fixtures.
+* ``build_work_queue`` -- reference :240-297 (vectorised like the reference:
+  repeat + local position).  Pinned by a brute-force triple loop on random
+  inputs, by the coverage invariant (every expert row x column is covered by
+  exactly one tile), by the queue lengths quoted for the BASELINE configs, and
+  by hand-enumerated cases.
+* ``grouped_gemm`` -- reference :446-457 (per-expert loop), computed in fp32 or
+  fp64.  Pinned by a brute-force scalar triple loop on tiny inputs, one-hot
+  rows (which select rows of B[e] and expose transposed operands or wrong
+  experts), expert-scaled identities, E=1 reducing to a plain matmul, and
+  integer-valued inputs with exact expected outputs.
+* ``queue_coverage`` -- the coverage invariant itself (a counting check).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+__all__ = [
+    "expert_offsets_from_recv_counts",
+    "build_work_queue",
+    "queue_length",
+    "grouped_gemm",
+    "queue_coverage",
+    "bf16_bits_to_f32",
+    "f32_to_bf16_bits",
+]
+
+
+def expert_offsets_from_recv_counts(counts, dtype=np.int32) -> np.ndarray:
+    """[0, c0, c0+c1, ...] of length E+1 (reference :315-323).
+
+    Each count is narrowed to int32 (``.to(torch.int32)``), the prefix sum is
+    taken in int64 (torch's integer cumsum) and the result cast to ``dtype``
+    (an int32 result wraps modulo 2**32).
+    """
+    c = np.asarray(counts)
+    if c.dtype.kind == "f":
+        c = np.trunc(c)
+    c32 = c.astype(np.int64).astype(np.int32).reshape(-1)
+    cum = np.cumsum(c32.astype(np.int64), dtype=np.int64)
+    out = np.concatenate([np.zeros(1, np.int64), cum])
+    return out.astype(dtype)
+
+
+def queue_length(offsets, n_size: int, block_m: int, block_n: int) -> int:
+    off = np.asarray(offsets, dtype=np.int64)
+    if off.size <= 1:
+        return 0
+    counts = np.clip(off[1:] - off[:-1], 0, None)
+    tiles_m = (counts + block_m - 1) // block_m
+    tiles_n = (int(n_size) + block_n - 1) // block_n
+    return int(tiles_m.sum()) * tiles_n
+
+
+def build_work_queue(offsets, n_size: int, block_m: int, block_n: int):
+    """(expert, tile_m, tile_n) int32 arrays (reference :253-292).
+
+    Per expert: count = max(off[e+1]-off[e], 0), ceil(count/block_m) m-tiles
+    times ceil(n_size/block_n) n-tiles, listed expert-major, then tile_m, then
+    tile_n (fastest).
+    """
+    off = np.asarray(offsets, dtype=np.int64)
+    num_experts = max(off.size - 1, 0)
+    counts = np.clip(off[1:] - off[:-1], 0, None) if num_experts else np.zeros(0, np.int64)
+    tiles_m = (counts + block_m - 1) // block_m
+    tiles_n = (int(n_size) + block_n - 1) // block_n
+    per_expert = tiles_m * tiles_n
+    total = int(per_expert.sum())
+    if total == 0:
+        z = np.zeros(0, np.int32)
+        return z, z.copy(), z.copy()
+    expert = np.repeat(np.arange(num_experts, dtype=np.int64), per_expert)
+    first = np.cumsum(per_expert) - per_expert
+    local = np.arange(total, dtype=np.int64) - first[expert]
+    return (
+        expert.astype(np.int32),
+        (local // tiles_n).astype(np.int32),
+        (local % tiles_n).astype(np.int32),
+    )
+
+
+def queue_coverage(offsets, m_size: int, n_size: int, block_m: int, block_n: int, queue):
+    """How many tiles of `queue` write each element of C [m_size, n_size].
+
+    A tile (e, tm, tn) writes rows off[e] + tm*block_m + [0, block_m) that lie
+    below off[e+1], and columns tn*block_n + [0, block_n) below n_size (the
+    store mask of reference :96-98).
+    """
+    off = np.asarray(offsets, dtype=np.int64)
+    cover = np.zeros((m_size, n_size), np.int32)
+    for e, tm, tn in zip(*queue):
+        r0 = off[e] + int(tm) * block_m
+        r1 = min(r0 + block_m, off[e + 1])
+        c0 = int(tn) * block_n
+        c1 = min(c0 + block_n, n_size)
+        if r1 > r0 and c1 > c0:
+            cover[r0:r1, c0:c1] += 1
+    return cover
+
+
+def grouped_gemm(a, b, offsets, acc_dtype=np.float32, out=None) -> np.ndarray:
+    """out[s:t] = a[s:t] @ b[e] for each expert with t > s (reference :449-456).
+
+    ``a`` [M, K] and ``b`` [E, K, N] are real arrays (bf16 inputs arrive
+    already widened to float32, exactly).  The product is computed in
+    ``acc_dtype``.  Rows outside every expert range keep the value of ``out``
+    (NaN when ``out`` is None), the counterpart of the reference's
+    uninitialised ``torch.empty`` rows.
+    """
+    a = np.asarray(a)
+    b = np.asarray(b)
+    off = np.asarray(offsets, dtype=np.int64)
+    if out is None:
+        out = np.full((a.shape[0], b.shape[2]), np.nan, dtype=acc_dtype)
+    for e in range(b.shape[0]):
+        s, t = int(off[e]), int(off[e + 1])
+        if t <= s:
+            continue
+        out[s:t] = a[s:t].astype(acc_dtype) @ b[e].astype(acc_dtype)
+    return out
+
+
+def bf16_bits_to_f32(bits) -> np.ndarray:
+    """Widen raw bf16 bit patterns (uint16) to float32 (exact)."""
+    u = np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16
+    return u.view(np.float32)
+
+
+def f32_to_bf16_bits(x) -> np.ndarray:
+    """Round float32 to bf16 bit patterns, nearest-even (NaN stays NaN)."""
+    x = np.asarray(x, dtype=np.float32)
+    u = x.reshape(-1).view(np.uint32).astype(np.uint64)
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    out = rounded.astype(np.uint16)
+    out[np.isnan(x.reshape(-1))] = 0x7FC0
+    return out.reshape(x.shape)

@@ -1,0 +1,74 @@
+"""The drop-in module's host-side behaviour (no GPU): the reference's
+ValueError conditions, CPU-tensor paths of the two integer builders (which run
+in libmgg's host code) against the oracle, and the FIFO queue cache."""
+import numpy as np
+import pytest
+import torch
+
+import grouped_gemm as gg
+import triton_grouped_gemm as tgg
+from oracle import grouped_gemm_oracle as orc
+
+
+def test_alias_module_exports_reference_names():
+    for name in ("persistent_grouped_gemm", "expert_offsets_from_recv_counts",
+                 "reference_grouped_gemm", "_build_work_queue"):
+        assert getattr(tgg, name) is getattr(gg, name)
+
+
+def test_gemm_requires_gpu_tensors():
+    a = torch.zeros(4, 8, dtype=torch.bfloat16)
+    b = torch.zeros(1, 8, 8, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="requires CUDA tensors"):
+        gg.persistent_grouped_gemm(a, b, torch.tensor([0, 4], dtype=torch.int32))
+
+
+@pytest.mark.parametrize("counts", [[], [0], [5], [3, 0, 5], [128] * 8, list(range(40))])
+@pytest.mark.parametrize("as_tensor", [False, True])
+def test_offsets_cpu_match_oracle(counts, as_tensor):
+    src = torch.tensor(counts, dtype=torch.int64) if as_tensor else counts
+    got = gg.expert_offsets_from_recv_counts(src)
+    assert got.dtype == torch.int32 and got.device.type == "cpu"
+    np.testing.assert_array_equal(got.numpy(), orc.expert_offsets_from_recv_counts(counts))
+
+
+def test_offsets_cpu_dtypes_and_shapes():
+    t = torch.tensor([[1, 2], [3, 4]], dtype=torch.int16)
+    assert gg.expert_offsets_from_recv_counts(t).tolist() == [0, 1, 3, 6, 10]
+    f = torch.tensor([1.9, 2.2])  # float counts truncate, as .to(int32) does
+    assert gg.expert_offsets_from_recv_counts(f).tolist() == [0, 1, 3]
+    big = torch.tensor([2**31 - 1, 1], dtype=torch.int64)
+    assert gg.expert_offsets_from_recv_counts(big).tolist() == [0, 2**31 - 1, -(2**31)]
+    out64 = gg.expert_offsets_from_recv_counts(big, dtype=torch.int64)
+    assert out64.dtype == torch.int64 and out64.tolist() == [0, 2**31 - 1, 2**31]
+    assert gg.expert_offsets_from_recv_counts([1, 2], dtype=torch.float32).tolist() == [0.0, 1.0, 3.0]
+
+
+@pytest.mark.parametrize("counts,n,bm,bn", [
+    ([3, 0, 5], 5, 2, 2), ([128] * 8, 1024, 128, 128), ([0, 0, 586, 3269, 7, 4331], 4096, 256, 256),
+    ([], 64, 64, 64), ([0, 0], 64, 64, 64), ([9], 0, 4, 4),
+])
+def test_queue_cpu_match_oracle(counts, n, bm, bn):
+    offs = torch.tensor(np.concatenate([[0], np.cumsum(counts)]).astype(np.int64))
+    got = gg._build_work_queue(offs, n, bm, bn)
+    for g, w in zip(got, orc.build_work_queue(offs.numpy(), n, bm, bn)):
+        assert g.dtype == torch.int32
+        np.testing.assert_array_equal(g.numpy(), w)
+
+
+def test_queue_cache_hits_and_fifo_eviction():
+    gg._WORK_QUEUE_CACHE.clear()
+    off = torch.tensor([0, 7, 7, 20], dtype=torch.int32)
+    q1 = gg._build_work_queue(off, 64, 4, 32)
+    q2 = gg._build_work_queue(off.to(torch.int64), 64, 4, 32)  # same key bytes (int64 view)
+    assert all(x is y for x, y in zip(q1, q2))
+    first_key = next(iter(gg._WORK_QUEUE_CACHE))
+    for i in range(gg._WORK_QUEUE_CACHE_MAX):
+        gg._build_work_queue(torch.tensor([0, i + 1]), 64, 4, 32)
+    assert len(gg._WORK_QUEUE_CACHE) == gg._WORK_QUEUE_CACHE_MAX
+    assert first_key not in gg._WORK_QUEUE_CACHE
+
+
+def test_flops_helper():
+    assert gg.grouped_gemm_flops(torch.tensor([0, 512, 1024]), 2048, 4096) == 2 * 1024 * 2048 * 4096
+    assert gg.grouped_gemm_flops([0, 5, 3], 8, 8) == 2 * 5 * 64  # negative counts add nothing

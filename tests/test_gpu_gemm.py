@@ -1,0 +1,250 @@
+"""GPU parity of the HIP grouped GEMM (through libmgg's C ABI) against the CPU
+oracle, plus the kernel's scheduling and counter semantics.
+
+Tolerance: max |C - C_fp32| <= 2e-2 * sqrt(K / 512) for
+bf16/fp16 outputs against an fp32/fp64 reference on the same (already
+rounded) inputs, over every row inside an expert range.
+"""
+import ctypes
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import grouped_gemm as gg
+import mgg_native as nat
+import workloads
+from oracle import grouped_gemm_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def tol(k):
+    return 2e-2 * math.sqrt(max(k, 1) / 512)
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_inputs(counts, k, n, dtype, device, seed=0, extra_rows=0):
+    gen = torch.Generator().manual_seed(seed)
+    m = int(sum(counts)) + extra_rows
+    a = torch.randn(m, k, generator=gen).to(dtype)
+    b = (torch.randn(len(counts), k, n, generator=gen) / math.sqrt(max(k, 1))).to(dtype)
+    offs = torch.tensor(orc.expert_offsets_from_recv_counts(counts), dtype=torch.int32)
+    return a.to(device), b.to(device), offs.to(device)
+
+
+def oracle_out(a, b, offs, rows=None):
+    a32 = a.float().cpu().numpy()
+    b32 = b.float().cpu().numpy()
+    return orc.grouped_gemm(a32, b32, offs.cpu().numpy(), acc_dtype=np.float64)
+
+
+def covered_rows(offs):
+    o = offs.cpu().numpy().astype(np.int64)
+    mask = np.zeros(int(max(o.max(initial=0), 0)), bool)
+    for e in range(len(o) - 1):
+        if o[e + 1] > o[e]:
+            mask[o[e]:o[e + 1]] = True
+    return mask
+
+
+def assert_parity(c, a, b, offs, k):
+    want = oracle_out(a, b, offs)
+    mask = covered_rows(offs)
+    got = c.float().cpu().numpy()[: mask.size][mask]
+    ref = want[: mask.size][mask]
+    err = float(np.abs(got - ref).max()) if got.size else 0.0
+    assert np.isfinite(got).all()
+    assert err <= tol(k), f"max abs err {err} > {tol(k)}"
+    return err
+
+
+SMALL_CASES = [
+    # counts, K, N
+    ([3, 0, 5], 64, 64),
+    ([1, 200, 0, 77, 300], 128, 192),
+    ([0, 0, 513, 0], 256, 136),          # one ragged expert, N edge inside a tile
+    ([130, 1, 257], 72, 64),             # K tail (72 = 64 + 8)
+    ([64] * 4, 2048, 256),
+    ([600], 520, 520),
+]
+
+
+@pytest.mark.parametrize("case", range(len(SMALL_CASES)))
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_small_ragged_parity_all_modes(cuda_device, case, dtype):
+    counts, k, n = SMALL_CASES[case]
+    a, b, offs = make_inputs(counts, k, n, dtype, cuda_device, seed=case, extra_rows=3)
+    outs = {}
+    for blocks in [(256, 256), (128, 128), (64, 64), (256, 128), (128, 256), (64, 256)]:
+        for atomic in (False, True):
+            for queue in ("device", "prebuilt"):
+                log(f"case={case} dtype={dtype} blocks={blocks} atomic={atomic} queue={queue}")
+                c = gg.persistent_grouped_gemm(a, b, offs, block_m=blocks[0], block_n=blocks[1],
+                                               use_atomic_queue=atomic, queue=queue)
+                torch.cuda.synchronize()
+                assert_parity(c, a, b, offs, k)
+                outs[(blocks, atomic, queue)] = c
+    # Each tile is computed the same way whatever the schedule: bitwise equal.
+    mask = torch.from_numpy(covered_rows(offs)).to(cuda_device)
+    for blocks in [(256, 256), (128, 128)]:
+        ref = outs[(blocks, False, "device")][: mask.numel()][mask]
+        for atomic in (False, True):
+            for queue in ("device", "prebuilt"):
+                got = outs[(blocks, atomic, queue)][: mask.numel()][mask]
+                assert torch.equal(got, ref), (blocks, atomic, queue)
+
+
+def test_cpu_plumbing_config_in_bf16(cuda_device):
+    case = workloads.make_case("cpu_plumbing", device="cpu", dtype=torch.bfloat16)
+    offs = gg.expert_offsets_from_recv_counts(case.counts, device=cuda_device)
+    a, b = case.a.to(cuda_device), case.b.to(cuda_device)
+    for atomic in (False, True):
+        c = gg.persistent_grouped_gemm(a, b, offs, block_m=128, block_n=128, use_atomic_queue=atomic)
+        assert_parity(c, a, b, offs, case.k)
+
+
+def sampled_parity(c, case, offs, stride=16):
+    """Full-size check: every `stride`-th row against the oracle (fp64)."""
+    rows = np.arange(0, case.m, stride)
+    a32 = case.a.float().cpu().numpy()
+    b32 = case.b.float().cpu().numpy()
+    o = offs.cpu().numpy().astype(np.int64)
+    expert = np.searchsorted(o, rows, side="right") - 1
+    got = c.float().cpu().numpy()[rows]
+    err = 0.0
+    for e in np.unique(expert):
+        sel = expert == e
+        ref = a32[rows[sel]].astype(np.float64) @ b32[e].astype(np.float64)
+        err = max(err, float(np.abs(got[sel] - ref).max()))
+    assert err <= tol(case.k), f"max abs err {err} > {tol(case.k)}"
+    return err
+
+
+@pytest.mark.parametrize("name", ["uniform", "skewed"])
+def test_full_size_configs(cuda_device, name):
+    case = workloads.make_case(name, device="cpu", dtype=torch.bfloat16)
+    log(f"full-size {name}: M={case.m}")
+    offs = gg.expert_offsets_from_recv_counts(case.counts, device=cuda_device)
+    case_gpu_a, case_gpu_b = case.a.to(cuda_device), case.b.to(cuda_device)
+    ref32 = None
+    outs = []
+    for blocks in [(256, 256), (128, 128)]:
+        for atomic in (False, True):
+            log(f"  blocks={blocks} atomic={atomic}")
+            c = gg.persistent_grouped_gemm(case_gpu_a, case_gpu_b, offs, block_m=blocks[0],
+                                           block_n=blocks[1], use_atomic_queue=atomic)
+            torch.cuda.synchronize()
+            sampled_parity(c, case, offs)
+            outs.append(c)
+    # Whole output against a float32 per-expert torch loop on the device.
+    ref32 = gg.reference_grouped_gemm(case_gpu_a.float(), case_gpu_b.float(), offs)
+    for c in outs:
+        err = (c.float() - ref32).abs().max().item()
+        assert err <= tol(case.k), err
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[2], outs[3])
+
+
+def test_empty_queue_zero_fills_and_keeps_counter(cuda_device):
+    a, b, offs = make_inputs([0, 0, 0], 64, 64, torch.bfloat16, cuda_device, extra_rows=5)
+    counter = torch.full((1,), 77, dtype=torch.int32, device=cuda_device)
+    for queue in ("device", "prebuilt"):
+        c = gg.persistent_grouped_gemm(a, b, offs, use_atomic_queue=True, work_counter=counter,
+                                       queue=queue)
+        torch.cuda.synchronize()
+        assert c.shape == (5, 64) and bool((c == 0).all())
+        assert counter.item() == 77  # untouched, as when the reference returns early
+    # No experts at all.
+    c = gg.persistent_grouped_gemm(a, b[:0], offs[:1])
+    assert bool((c == 0).all())
+
+
+@pytest.mark.parametrize("num_sms", [1, 7, 64, 256, 1000])
+def test_work_counter_final_value(cuda_device, num_sms):
+    counts = [300, 0, 129, 511]
+    a, b, offs = make_inputs(counts, 128, 256, torch.bfloat16, cuda_device)
+    counter = torch.zeros(1, dtype=torch.int32, device=cuda_device)
+    w = orc.queue_length(offs.cpu().numpy(), 256, 128, 128)
+    for rep in range(3):  # the library counter must be back at zero between calls
+        c = gg.persistent_grouped_gemm(a, b, offs, num_sms=num_sms, block_m=128, block_n=128,
+                                       use_atomic_queue=True, work_counter=counter)
+        torch.cuda.synchronize()
+        assert counter.item() == w + num_sms, (rep, counter.item())
+        assert_parity(c, a, b, offs, 128)
+
+
+def test_striped_with_few_workers(cuda_device):
+    a, b, offs = make_inputs([100, 250, 3], 96, 320, torch.float16, cuda_device)
+    for g in (1, 3, 9):
+        c = gg.persistent_grouped_gemm(a, b, offs, num_sms=g, use_atomic_queue=False)
+        assert_parity(c, a, b, offs, 96)
+
+
+def test_odd_shapes_are_padded(cuda_device):
+    a, b, offs = make_inputs([17, 0, 40], 50, 37, torch.bfloat16, cuda_device)
+    c = gg.persistent_grouped_gemm(a, b, offs)
+    assert c.shape == (57, 37) and c.is_contiguous()
+    assert_parity(c, a, b, offs, 50)
+
+
+def test_strided_operands(cuda_device):
+    a_wide, b, offs = make_inputs([33, 70], 128, 64, torch.bfloat16, cuda_device)
+    big = torch.randn(103, 256, device=cuda_device).to(torch.bfloat16)
+    big[:, 64:192] = a_wide
+    a_view = big[:, 64:192]  # row stride 256, 16-byte aligned
+    assert a_view.stride() == (256, 1)
+    bt = b.transpose(1, 2).contiguous().transpose(1, 2)  # N not contiguous -> copied
+    c = gg.persistent_grouped_gemm(a_view, bt, offs)
+    assert_parity(c, a_wide, b, offs, 128)
+
+
+def test_rows_outside_experts_are_not_written(cuda_device):
+    """Calls the C ABI directly with a sentinel-filled C."""
+    a, b, offs = make_inputs([5, 0, 9], 64, 128, torch.bfloat16, cuda_device, extra_rows=0)
+    m = 20
+    a_full = torch.zeros(m, 64, dtype=torch.bfloat16, device=cuda_device)
+    a_full[2:16] = a
+    offs_shift = (offs + 2).to(torch.int32)  # rows [2, 16) covered, others not
+    c = torch.full((m, 128), 123.0, dtype=torch.bfloat16, device=cuda_device)
+    for atomic in (0, 1):
+        nat.check(nat.lib().mgg_grouped_gemm(
+            nat.MGG_DTYPE_BF16, a_full.data_ptr(), b.data_ptr(), c.data_ptr(), offs_shift.data_ptr(),
+            m, 64, 128, 3, 64, 64 * 128, 128, 128, None, None, None, -1, 64, 64, 5, atomic, None,
+            torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        assert bool((c[:2] == 123).all()) and bool((c[16:] == 123).all())
+        want = oracle_out(a, b, offs)
+        assert float(np.abs(c[2:16].float().cpu().numpy() - want).max()) <= tol(64)
+
+
+def test_device_queue_builder_bit_exact(cuda_device):
+    data = np.load(__import__("pathlib").Path(__file__).parent / "golden" / "queues.npz",
+                   allow_pickle=False)
+    tags = sorted({k.rsplit("__", 1)[0] for k in data.files if not k.endswith("__offsets")})
+    for tag in tags:
+        name, n_part, tile = tag.split("__")
+        bm, bn = map(int, tile.split("x"))
+        offs = torch.from_numpy(data[f"{name}__offsets"]).to(cuda_device)
+        gg._WORK_QUEUE_CACHE.clear()
+        q = gg._build_work_queue(offs, int(n_part[1:]), bm, bn)
+        for arr, suffix in zip(q, ("expert", "tile_m", "tile_n")):
+            np.testing.assert_array_equal(arr.cpu().numpy(), data[f"{tag}__{suffix}"], err_msg=tag)
+
+
+def test_device_offsets_bit_exact(cuda_device):
+    rng = np.random.default_rng(5)
+    for size in (0, 1, 16, 1000, 5000):
+        for src_dtype in (torch.int32, torch.int64):
+            counts = rng.integers(0, 3000, size)
+            t = torch.from_numpy(counts).to(src_dtype).to(cuda_device)
+            for out_dtype in (torch.int32, torch.int64):
+                got = gg.expert_offsets_from_recv_counts(t, dtype=out_dtype)
+                want = orc.expert_offsets_from_recv_counts(counts, dtype=np.int32 if out_dtype == torch.int32 else np.int64)
+                np.testing.assert_array_equal(got.cpu().numpy(), want)
+    wrap = torch.tensor([2**31 - 1, 1, 2**32 + 3], dtype=torch.int64, device=cuda_device)
+    assert gg.expert_offsets_from_recv_counts(wrap).tolist() == [0, 2**31 - 1, -(2**31), -(2**31) + 3]
