@@ -217,7 +217,7 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   // their results are never stored.
   int64_t b_col = 8 * b_ng;
   b_col = n0 + b_col > p.n - 8 ? p.n - 8 - n0 : b_col;
-  const uint32_t b_voff = has_b ? (uint32_t)((8 * b_kg * p.ldb_k + b_col) * 2) : kOutOfRange;
+  const uint32_t b_voff = (uint32_t)((8 * b_kg * p.ldb_k + b_col) * 2);
   const uint32_t b_row = (uint32_t)(p.ldb_k * 2);
 
   u32x4 a_reg[kAChunks];
@@ -230,9 +230,11 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
     const int a_s = (int)(k0 * 2);
 #pragma unroll
     for (int i = 0; i < kAChunks; ++i) a_reg[i] = bload(a_rsrc, a_voff + i * a_pass, a_s);
-    const int b_s = (int)((uint32_t)k0 * b_row);
+    if (has_b) {  // threads past the BN blocks issue no B loads
+      const int b_s = (int)((uint32_t)k0 * b_row);
 #pragma unroll
-    for (int s = 0; s < 8; ++s) b_reg[s] = bload(b_rsrc, b_voff + s * b_row, b_s);
+      for (int s = 0; s < 8; ++s) b_reg[s] = bload(b_rsrc, b_voff + s * b_row, b_s);
+    }
   };
   // The last, partial stage: the whole offset goes through the VGPR so the
   // descriptor's range check zeroes A columns and B rows at k >= K.
@@ -241,10 +243,12 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
 #pragma unroll
     for (int i = 0; i < kAChunks; ++i)
       a_reg[i] = bload(a_rsrc, a_in ? a_voff + (uint32_t)(k0 * 2) + i * a_pass : kOutOfRange, 0);
+    if (has_b) {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const bool b_in = has_b && k0 + 8 * b_kg + s < K;
-      b_reg[s] = bload(b_rsrc, b_in ? b_voff + ((uint32_t)k0 + s) * b_row : kOutOfRange, 0);
+      for (int s = 0; s < 8; ++s) {
+        const bool b_in = k0 + 8 * b_kg + s < K;
+        b_reg[s] = bload(b_rsrc, b_in ? b_voff + ((uint32_t)k0 + s) * b_row : kOutOfRange, 0);
+      }
     }
   };
 

@@ -3,7 +3,11 @@ oracle, plus the kernel's scheduling and counter semantics.
 
 Tolerance: max |C - C_fp32| <= 2e-2 * sqrt(K / 512) for
 bf16/fp16 outputs against an fp32/fp64 reference on the same (already
-rounded) inputs, over every row inside an expert range.
+rounded) inputs, over every row inside an expert range.  K is floored at 512
+in the formula: with N(0, 1/K) weights the outputs are O(1) at every K, and
+rounding them to bf16 alone costs up to half an ulp, 2^-6 = 0.0156 for
+|y| in [4, 8), which is above 2e-2 * sqrt(K/512) for K < 512.  Every
+BASELINE config has K >= 512, where the formula applies unchanged.
 """
 import ctypes
 import math
@@ -22,7 +26,7 @@ pytestmark = pytest.mark.gpu
 
 
 def tol(k):
-    return 2e-2 * math.sqrt(max(k, 1) / 512)
+    return 2e-2 * math.sqrt(max(k, 512) / 512)
 
 
 def log(msg):
