@@ -158,6 +158,8 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   constexpr int kNB = BN / 64;                 // 32-col MFMA blocks per wave
   constexpr int kAChunks = BM * 8 / kThreads;  // 16-byte A chunks per thread per stage
   constexpr int kARowsPerPass = kThreads / 8;  // A rows covered by one pass of the block
+  constexpr int kBRows = BN / 32;              // K rows of B per thread per stage
+  constexpr int kKGroups = kBK / kBRows;       // threads along K in the B load
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -210,18 +212,19 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   const int a_kc = tid & 7;  // 16-byte chunk (8 K values) this thread loads
   const uint32_t a_voff = (uint32_t)(((tid >> 3) * p.lda + a_kc * 8) * 2);
   const uint32_t a_pass = (uint32_t)(kARowsPerPass * p.lda * 2);  // bytes between passes
-  const bool has_b = tid < BN;  // BN blocks of 8(k) x 8(n) per stage
-  const int b_kg = tid & 7;     // k group: rows 8*b_kg .. +7 of the stage
-  const int b_ng = tid >> 3;    // n group: columns 8*b_ng .. +7 of the tile
+  // B: every thread loads a kBRows(k) x 8(n) block, kBRows = 8, 4, 2 for
+  // BN = 256, 128, 64, so all 256 threads take part and no load is predicated.
+  const int b_kg = tid % kKGroups;  // k group: rows kBRows*b_kg .. + kBRows-1
+  const int b_ng = tid / kKGroups;  // n group: columns 8*b_ng .. +7 of the tile
   // Columns past N (edge tiles) are clamped onto column N-8: in bounds, and
   // their results are never stored.
   int64_t b_col = 8 * b_ng;
   b_col = n0 + b_col > p.n - 8 ? p.n - 8 - n0 : b_col;
-  const uint32_t b_voff = (uint32_t)((8 * b_kg * p.ldb_k + b_col) * 2);
+  const uint32_t b_voff = (uint32_t)((kBRows * b_kg * p.ldb_k + b_col) * 2);
   const uint32_t b_row = (uint32_t)(p.ldb_k * 2);
 
   u32x4 a_reg[kAChunks];
-  u32x4 b_reg[8];
+  u32x4 b_reg[kBRows];
 
   // A full stage (k0 + 64 <= K): every B row and every A column is in range,
   // so the uniform stage offset rides in the SGPR offset; rows of A past M
@@ -230,11 +233,9 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
     const int a_s = (int)(k0 * 2);
 #pragma unroll
     for (int i = 0; i < kAChunks; ++i) a_reg[i] = bload(a_rsrc, a_voff + i * a_pass, a_s);
-    if (has_b) {  // threads past the BN blocks issue no B loads
-      const int b_s = (int)((uint32_t)k0 * b_row);
+    const int b_s = (int)((uint32_t)k0 * b_row);
 #pragma unroll
-      for (int s = 0; s < 8; ++s) b_reg[s] = bload(b_rsrc, b_voff + s * b_row, b_s);
-    }
+    for (int s = 0; s < kBRows; ++s) b_reg[s] = bload(b_rsrc, b_voff + s * b_row, b_s);
   };
   // The last, partial stage: the whole offset goes through the VGPR so the
   // descriptor's range check zeroes A columns and B rows at k >= K.
@@ -243,12 +244,10 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
 #pragma unroll
     for (int i = 0; i < kAChunks; ++i)
       a_reg[i] = bload(a_rsrc, a_in ? a_voff + (uint32_t)(k0 * 2) + i * a_pass : kOutOfRange, 0);
-    if (has_b) {
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const bool b_in = k0 + 8 * b_kg + s < K;
-        b_reg[s] = bload(b_rsrc, b_in ? b_voff + ((uint32_t)k0 + s) * b_row : kOutOfRange, 0);
-      }
+    for (int s = 0; s < kBRows; ++s) {
+      const bool b_in = k0 + kBRows * b_kg + s < K;
+      b_reg[s] = bload(b_rsrc, b_in ? b_voff + ((uint32_t)k0 + s) * b_row : kOutOfRange, 0);
     }
   };
 
@@ -258,22 +257,30 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
 #pragma unroll
     for (int i = 0; i < kAChunks; ++i)
       lds_store(la, lds_off((tid >> 3) + kARowsPerPass * i, a_kc), a_reg[i]);
-    if (has_b) {
-      // 8x8 transpose of 16-bit values: b_reg[s].d[j] holds columns 2j, 2j+1
-      // of k row s; column t gets k rows 0..7 as four packed pairs.
-      u32x4 col[8];
+    // kBRows x 8 transpose of 16-bit values: b_reg[s][j] holds columns 2j,
+    // 2j+1 of k row s; column t gets its kBRows k values as packed pairs.
+    uint32_t col[8][kBRows / 2];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 4; ++j) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t x = b_reg[2 * q][j];
-          const uint32_t y = b_reg[2 * q + 1][j];
-          col[2 * j][q] = __builtin_amdgcn_perm(y, x, 0x05040100u);
-          col[2 * j + 1][q] = __builtin_amdgcn_perm(y, x, 0x07060302u);
-        }
+      for (int q = 0; q < kBRows / 2; ++q) {
+        const uint32_t x = b_reg[2 * q][j];
+        const uint32_t y = b_reg[2 * q + 1][j];
+        col[2 * j][q] = __builtin_amdgcn_perm(y, x, 0x05040100u);
+        col[2 * j + 1][q] = __builtin_amdgcn_perm(y, x, 0x07060302u);
       }
+    }
+    const int b_byte = b_kg * kBRows * 2;  // byte offset of this k group in an LDS row
 #pragma unroll
-      for (int t = 0; t < 8; ++t) lds_store(lb, lds_off(8 * b_ng + t, b_kg), col[t]);
+    for (int t = 0; t < 8; ++t) {
+      uint8_t* dst = lb + (8 * b_ng + t) * kLdsRow + b_byte;
+      if constexpr (kBRows == 8) {
+        *reinterpret_cast<u32x4*>(dst) = u32x4{col[t][0], col[t][1], col[t][2], col[t][3]};
+      } else if constexpr (kBRows == 4) {
+        *reinterpret_cast<u32x2*>(dst) = u32x2{col[t][0], col[t][1]};
+      } else {
+        *reinterpret_cast<uint32_t*>(dst) = col[t][0];
+      }
     }
   };
 
@@ -306,28 +313,37 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
       for (int i = 0; i < kNB; ++i)
 #pragma unroll
         for (int j = 0; j < kMB; ++j) acc[i][j] = T::mfma(bfr[i], af[j], acc[i][j]);
-      // Keep the next sub-step's fragment loads from being hoisted above
-      // these MFMAs (bounds the live fragment registers to two sub-steps).
-      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
+  // Stage pipeline.  The steady-state loop loads only full stages, without
+  // branches around the loads, so their registers are first read by the LDS
+  // stores after the MFMAs and the loads stay in flight during the compute.
   const int nk = (int)((K + kBK - 1) / kBK);
   const int nk_full = (int)(K / kBK);  // stages with k0 + 64 <= K
   if (nk_full > 0) load_full(0); else load_tail(0);
+  __syncthreads();  // the previous tile's waves are done with the LDS stages
   store_stage(0);
   __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      if (kt + 1 < nk_full) load_full((int64_t)(kt + 1) * kBK);
-      else load_tail((int64_t)(kt + 1) * kBK);
-    }
-    compute_stage(buf);
-    if (more) store_stage(buf ^ 1);
+  int kt = 0;
+  for (; kt + 1 < nk_full; ++kt) {
+    load_full((int64_t)(kt + 1) * kBK);
+    // Keep the loads issued before the MFMAs (the scheduler would otherwise
+    // sink them next to their use and expose their latency).
+    __builtin_amdgcn_sched_barrier(0);
+    compute_stage(kt & 1);
+    __builtin_amdgcn_sched_barrier(0);
+    store_stage((kt + 1) & 1);
     __syncthreads();
   }
+  if (kt + 1 < nk) {  // the partial last stage when K % 64 != 0
+    load_tail((int64_t)(kt + 1) * kBK);
+    compute_stage(kt & 1);
+    store_stage((kt + 1) & 1);
+    __syncthreads();
+    ++kt;
+  }
+  if (nk > 0) compute_stage(kt & 1);
 
   // ---- epilogue: acc[i][j] register r holds D[n][m] of the 32x32 block with
   // n = 8*(r/4) + 4*(lane/32) + r%4, m = lane%32 (D = C^T).
