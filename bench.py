@@ -50,6 +50,9 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU oracle sample budget")
     p.add_argument("--profile-only", action="store_true",
                    help="only the warmup and timed steps (for rocprofv3 runs)")
+    p.add_argument("--calibrate-copy-mib", type=int, default=0,
+                   help="instead of the GEMM, run --steps plain device copies of this many MiB "
+                        "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -127,6 +130,15 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.calibrate_copy_mib:
+        n = args.calibrate_copy_mib * 1024 * 1024 // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": n * 4, "copies": args.warmup + args.steps}))
+        return
     case = workloads.make_case(args.workload, device=dev, dtype=torch.bfloat16)
     offs = gg.expert_offsets_from_recv_counts(case.counts, device=dev)
     atomic = args.mode == "atomic"

@@ -226,61 +226,53 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   u32x4 a_reg[kAChunks];
   u32x4 b_reg[kBRows];
 
-  // A full stage (k0 + 64 <= K): every B row and every A column is in range,
-  // so the uniform stage offset rides in the SGPR offset; rows of A past M
-  // are out of range through their VGPR offset alone.
-  auto load_full = [&](int64_t k0) {
-    const int a_s = (int)(k0 * 2);
-#pragma unroll
-    for (int i = 0; i < kAChunks; ++i) a_reg[i] = bload(a_rsrc, a_voff + i * a_pass, a_s);
-    const int b_s = (int)((uint32_t)k0 * b_row);
-#pragma unroll
-    for (int s = 0; s < kBRows; ++s) b_reg[s] = bload(b_rsrc, b_voff + s * b_row, b_s);
-  };
-  // The last, partial stage: the whole offset goes through the VGPR so the
+  // One global load of the next stage: l < kAChunks is A chunk l, else B row
+  // l - kAChunks.  A full stage (k0 + 64 <= K) has every B row and every A
+  // column in range, so the uniform stage offset rides in the SGPR offset and
+  // rows of A past M fall out of range through their VGPR offset alone.  In
+  // the partial last stage the whole offset goes through the VGPR, so the
   // descriptor's range check zeroes A columns and B rows at k >= K.
-  auto load_tail = [&](int64_t k0) {
-    const bool a_in = k0 + a_kc * 8 < K;
-#pragma unroll
-    for (int i = 0; i < kAChunks; ++i)
-      a_reg[i] = bload(a_rsrc, a_in ? a_voff + (uint32_t)(k0 * 2) + i * a_pass : kOutOfRange, 0);
-#pragma unroll
-    for (int s = 0; s < kBRows; ++s) {
-      const bool b_in = k0 + kBRows * b_kg + s < K;
-      b_reg[s] = bload(b_rsrc, b_in ? b_voff + ((uint32_t)k0 + s) * b_row : kOutOfRange, 0);
+  auto load_one = [&](int l, int64_t k0, bool tail) {
+    if (l < kAChunks) {
+      if (!tail) {
+        a_reg[l] = bload(a_rsrc, a_voff + l * a_pass, (int)(k0 * 2));
+      } else {
+        const bool in = k0 + a_kc * 8 < K;
+        a_reg[l] = bload(a_rsrc, in ? a_voff + (uint32_t)(k0 * 2) + l * a_pass : kOutOfRange, 0);
+      }
+    } else {
+      const int r = l - kAChunks;
+      if (!tail) {
+        b_reg[r] = bload(b_rsrc, b_voff + r * b_row, (int)((uint32_t)k0 * b_row));
+      } else {
+        const bool in = k0 + kBRows * b_kg + r < K;
+        b_reg[r] = bload(b_rsrc, in ? b_voff + ((uint32_t)k0 + r) * b_row : kOutOfRange, 0);
+      }
     }
   };
 
-  auto store_stage = [&](int buf) {
-    uint8_t* la = lds_a + buf * (BM * kLdsRow);
-    uint8_t* lb = lds_b + buf * (BN * kLdsRow);
-#pragma unroll
-    for (int i = 0; i < kAChunks; ++i)
-      lds_store(la, lds_off((tid >> 3) + kARowsPerPass * i, a_kc), a_reg[i]);
-    // kBRows x 8 transpose of 16-bit values: b_reg[s][j] holds columns 2j,
-    // 2j+1 of k row s; column t gets its kBRows k values as packed pairs.
-    uint32_t col[8][kBRows / 2];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int q = 0; q < kBRows / 2; ++q) {
-        const uint32_t x = b_reg[2 * q][j];
-        const uint32_t y = b_reg[2 * q + 1][j];
-        col[2 * j][q] = __builtin_amdgcn_perm(y, x, 0x05040100u);
-        col[2 * j + 1][q] = __builtin_amdgcn_perm(y, x, 0x07060302u);
-      }
+  // One LDS store of the next stage: s < kAChunks stores A chunk s; else
+  // column t = s - kAChunks of this thread's B block, transposed in registers
+  // (b_reg[q][t/2] holds columns t&~1, t|1 of k row q) into kBRows K values.
+  auto store_one = [&](int s, int buf) {
+    if (s < kAChunks) {
+      lds_store(lds_a + buf * (BM * kLdsRow), lds_off((tid >> 3) + kARowsPerPass * s, a_kc),
+                a_reg[s]);
+      return;
     }
-    const int b_byte = b_kg * kBRows * 2;  // byte offset of this k group in an LDS row
+    const int t = s - kAChunks;
+    const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;
+    uint32_t colv[kBRows / 2];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      uint8_t* dst = lb + (8 * b_ng + t) * kLdsRow + b_byte;
-      if constexpr (kBRows == 8) {
-        *reinterpret_cast<u32x4*>(dst) = u32x4{col[t][0], col[t][1], col[t][2], col[t][3]};
-      } else if constexpr (kBRows == 4) {
-        *reinterpret_cast<u32x2*>(dst) = u32x2{col[t][0], col[t][1]};
-      } else {
-        *reinterpret_cast<uint32_t*>(dst) = col[t][0];
-      }
+    for (int q = 0; q < kBRows / 2; ++q)
+      colv[q] = __builtin_amdgcn_perm(b_reg[2 * q + 1][t >> 1], b_reg[2 * q][t >> 1], sel);
+    uint8_t* dst = lds_b + buf * (BN * kLdsRow) + (8 * b_ng + t) * kLdsRow + b_kg * kBRows * 2;
+    if constexpr (kBRows == 8) {
+      *reinterpret_cast<u32x4*>(dst) = u32x4{colv[0], colv[1], colv[2], colv[3]};
+    } else if constexpr (kBRows == 4) {
+      *reinterpret_cast<u32x2*>(dst) = u32x2{colv[0], colv[1]};
+    } else {
+      *reinterpret_cast<uint32_t*>(dst) = colv[0];
     }
   };
 
@@ -296,54 +288,95 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   const int frag_half = lane >> 5;
   const int a_row_base = wm * (BM / 2) + frag_row;
   const int b_row_base = wn * (BN / 2) + frag_row;
-
-  auto compute_stage = [&](int buf) {
-    const uint8_t* la = lds_a + buf * (BM * kLdsRow);
-    const uint8_t* lb = lds_b + buf * (BN * kLdsRow);
-#pragma unroll
-    for (int kk = 0; kk < kBK / 16; ++kk) {
-      const int chunk = 2 * kk + frag_half;
-      u32x4 af[kMB];
-      u32x4 bfr[kNB];
-#pragma unroll
-      for (int j = 0; j < kMB; ++j) af[j] = lds_load(la, lds_off(a_row_base + 32 * j, chunk));
-#pragma unroll
-      for (int i = 0; i < kNB; ++i) bfr[i] = lds_load(lb, lds_off(b_row_base + 32 * i, chunk));
-#pragma unroll
-      for (int i = 0; i < kNB; ++i)
-#pragma unroll
-        for (int j = 0; j < kMB; ++j) acc[i][j] = T::mfma(bfr[i], af[j], acc[i][j]);
-    }
+  u32x4 fa[2][kMB];  // A fragments of two consecutive 16-wide K steps
+  u32x4 fb[2][kNB];  // B^T fragments
+  auto read_frag_a = [&](int buf, int kk, int slot, int j) {
+    fa[slot][j] = lds_load(lds_a + buf * (BM * kLdsRow),
+                           lds_off(a_row_base + 32 * j, 2 * kk + frag_half));
+  };
+  auto read_frag_b = [&](int buf, int kk, int slot, int i) {
+    fb[slot][i] = lds_load(lds_b + buf * (BN * kLdsRow),
+                           lds_off(b_row_base + 32 * i, 2 * kk + frag_half));
   };
 
-  // Stage pipeline.  The steady-state loop loads only full stages, without
-  // branches around the loads, so their registers are first read by the LDS
-  // stores after the MFMAs and the loads stay in flight during the compute.
+  // One K stage in explicit program order.  The stage's 4 K steps x 4 groups
+  // each issue a quarter of the K step's MFMAs followed by (a) a quarter of
+  // the next K step's fragment reads, (b) in the first 8 groups, 1/8 of the
+  // next stage's global loads, (c) in the last 8 groups, 1/8 of its
+  // transposes and LDS stores.  sched_barrier fences keep this order: a wave
+  // issues in order, so a burst of loads would stall its MFMAs behind a full
+  // memory queue, and fragment reads issued late would stall each MFMA.
+  // Fragments of K step 0 must already be in fa[0]/fb[0].
+  constexpr int kMfmaPerStep = kMB * kNB;
+  constexpr int kLoads = kAChunks + kBRows;
+  constexpr int kStores = kAChunks + 8;
+  auto stage = [&](int buf, int nbuf, int64_t k0_next, bool load_next, bool tail_next) {
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      const int cur = kk & 1;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+#pragma unroll
+        for (int p = g * kMfmaPerStep / 4; p < (g + 1) * kMfmaPerStep / 4; ++p) {
+          const int i = p / kMB, j = p % kMB;
+          acc[i][j] = T::mfma(fb[cur][i], fa[cur][j], acc[i][j]);
+        }
+        if (kk + 1 < kBK / 16) {
+#pragma unroll
+          for (int j = g; j < kMB; j += 4) read_frag_a(buf, kk + 1, cur ^ 1, j);
+#pragma unroll
+          for (int i = g; i < kNB; i += 4) read_frag_b(buf, kk + 1, cur ^ 1, i);
+        }
+        if (load_next) {
+          const int grp = kk * 4 + g;  // 0..15
+          if (grp < 8) {
+#pragma unroll
+            for (int l = grp * kLoads / 8; l < (grp + 1) * kLoads / 8; ++l)
+              load_one(l, k0_next, tail_next);
+          } else {
+#pragma unroll
+            for (int t = (grp - 8) * kStores / 8; t < (grp - 7) * kStores / 8; ++t)
+              store_one(t, nbuf);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  auto first_frags = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < kMB; ++j) read_frag_a(buf, 0, 0, j);
+#pragma unroll
+    for (int i = 0; i < kNB; ++i) read_frag_b(buf, 0, 0, i);
+  };
+
+  // Stage pipeline: stage kt computes from LDS buffer kt&1 while the next
+  // stage moves global -> registers -> LDS buffer (kt+1)&1; one barrier per
+  // stage.
   const int nk = (int)((K + kBK - 1) / kBK);
   const int nk_full = (int)(K / kBK);  // stages with k0 + 64 <= K
-  if (nk_full > 0) load_full(0); else load_tail(0);
+#pragma unroll
+  for (int l = 0; l < kLoads; ++l) load_one(l, 0, nk_full == 0);
   __syncthreads();  // the previous tile's waves are done with the LDS stages
-  store_stage(0);
+#pragma unroll
+  for (int t = 0; t < kStores; ++t) store_one(t, 0);
   __syncthreads();
   int kt = 0;
   for (; kt + 1 < nk_full; ++kt) {
-    load_full((int64_t)(kt + 1) * kBK);
-    // Keep the loads issued before the MFMAs (the scheduler would otherwise
-    // sink them next to their use and expose their latency).
-    __builtin_amdgcn_sched_barrier(0);
-    compute_stage(kt & 1);
-    __builtin_amdgcn_sched_barrier(0);
-    store_stage((kt + 1) & 1);
+    first_frags(kt & 1);
+    stage(kt & 1, (kt + 1) & 1, (int64_t)(kt + 1) * kBK, true, false);
     __syncthreads();
   }
   if (kt + 1 < nk) {  // the partial last stage when K % 64 != 0
-    load_tail((int64_t)(kt + 1) * kBK);
-    compute_stage(kt & 1);
-    store_stage((kt + 1) & 1);
+    first_frags(kt & 1);
+    stage(kt & 1, (kt + 1) & 1, (int64_t)(kt + 1) * kBK, true, true);
     __syncthreads();
     ++kt;
   }
-  if (nk > 0) compute_stage(kt & 1);
+  if (nk > 0) {
+    first_frags(kt & 1);
+    stage(kt & 1, 0, 0, false, false);
+  }
 
   // ---- epilogue: acc[i][j] register r holds D[n][m] of the 32x32 block with
   // n = 8*(r/4) + 4*(lane/32) + r%4, m = lane%32 (D = C^T).
