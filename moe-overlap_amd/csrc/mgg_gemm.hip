@@ -40,6 +40,9 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int kThreads = 256;
 constexpr int kBK = 64;                 // K elements per LDS stage
@@ -74,6 +77,9 @@ __device__ __forceinline__ int lds_off(int row, int chunk) { return row * kLdsRo
 
 __device__ __forceinline__ u32x4 lds_load(const uint8_t* base, int off) {
   return *reinterpret_cast<const u32x4*>(base + off);
+}
+__device__ __forceinline__ __attribute__((address_space(3))) uint8_t* lds_ptr(uint8_t* p) {
+  return (__attribute__((address_space(3))) uint8_t*)p;
 }
 __device__ __forceinline__ void lds_store(uint8_t* base, int off, u32x4 v) {
   *reinterpret_cast<u32x4*>(base + off) = v;
@@ -148,22 +154,77 @@ __device__ void zero_fill(const GemmParams& p) {
   }
 }
 
+// One 16-byte-per-lane DMA from global memory (through a buffer descriptor)
+// straight into LDS: lane l's 16 bytes land at LDS byte address
+// lds + 16*l, so a wave fills 1 KiB.  Issued from inline assembly so that the
+// compiler does not treat every later LDS read as dependent on it (it cannot
+// tell DMA targets apart and would wait for all of them); the kernel waits
+// on the DMA explicitly (wait_dma) before the barrier that publishes a stage.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// Waits until at most N of this wave's DMAs are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_dma() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ i32x4 make_rsrc4(const void* base, int64_t bytes) {
+  const int64_t cap = 0x7FFFFFF0LL;
+  const uint64_t addr = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = (int32_t)(uint32_t)addr;
+  r[1] = (int32_t)(uint32_t)((addr >> 32) & 0xFFFFu);  // stride 0
+  r[2] = (int32_t)(bytes < 0 ? 0 : (bytes > cap ? cap : bytes));
+  r[3] = 0x00020000;  // gfx9-family default format
+  return r;
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 // Computes one output tile.  All arguments are uniform across the workgroup,
 // so the early returns never split a barrier.
+//
+// K advances in stages of 32; four stages rotate through LDS.  A stage holds
+// A [BM x 32] as BM rows of 64 bytes and B [32 x BN] in its global layout
+// (K rows of BN contiguous N values); both arrive by DMA, three stages ahead
+// of the one being multiplied.  16-byte chunks are XOR-swizzled on the global
+// side so that the fragment reads below are bank-conflict free:
+//   A row r, chunk c  -> physical chunk c ^ ((r >> 2) & 3)
+//   B row k, chunk c  -> physical chunk c ^ 4*(k & 3)        (BN >= 128)
+//                                        c ^ 4*((k >> 1) & 1) (BN == 64)
+// A fragments are ds_read_b128 (8 consecutive K of one row).  B fragments use
+// the gfx950 transposing read ds_read_b64_tr_b16: in each group of 16 lanes,
+// lane s addresses B[k0 + s/4][n0 + 4*(s%4) .. +3] and lane j receives
+// B[k0 .. k0+3][n0 + j], so two reads give a lane the 8 consecutive K of its
+// column that the MFMA expects.
 template <int BM, int BN, class T>
 __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int n_tiles,
-                                         const int32_t* s_prefix, uint8_t* lds_a,
-                                         uint8_t* lds_b) {
-  constexpr int kMB = BM / 64;                 // 32-row MFMA blocks per wave
-  constexpr int kNB = BN / 64;                 // 32-col MFMA blocks per wave
-  constexpr int kAChunks = BM * 8 / kThreads;  // 16-byte A chunks per thread per stage
-  constexpr int kARowsPerPass = kThreads / 8;  // A rows covered by one pass of the block
-  constexpr int kBRows = BN / 32;              // K rows of B per thread per stage
-  constexpr int kKGroups = kBK / kBRows;       // threads along K in the B load
+                                         const int32_t* s_prefix, uint8_t* lds) {
+  constexpr int kBK = 32;                   // K per stage
+  constexpr int kStages = 4;                // LDS stages in rotation
+  constexpr int kAStage = BM * kBK * 2;     // bytes of A per stage
+  constexpr int kBStage = kBK * BN * 2;     // bytes of B per stage
+  constexpr int kBRowBytes = BN * 2;
+  constexpr int kAPerWave = BM / 64;        // A DMAs per wave per stage (16 rows each)
+  constexpr int kBPerWave = BN / 64;        // B DMAs per wave per stage
+  constexpr int kDmaPerStage = kAPerWave + kBPerWave;
+  constexpr int kBChunks = BN / 8;          // 16-byte chunks per B row
+  constexpr int kBRowsPerDma = 64 / kBChunks;
+  constexpr int kMB = BM / 64;              // 32-row MFMA blocks per wave
+  constexpr int kNB = BN / 64;              // 32-col MFMA blocks per wave
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1;
   const int wn = wave >> 1;
 
@@ -196,85 +257,88 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   const int64_t K = p.k;
   const int64_t last_row = p.m - 1;
 
-  // ---- global sources: raw buffer descriptors (uniform, per tile) --------
+  // ---- global sources ----------------------------------------------------
   // Each descriptor ends exactly at the last element of its operand, so a
-  // 16-byte load past it returns zeros: rows of A past M, rows of B past K
-  // and the B columns past N of the last row.  Rows of A inside [0, M) but
-  // past this expert's count load the next expert's data; their results are
-  // never stored.  Offsets stay 32-bit (the host bounds lda, ldb_k).
+  // DMA past it writes zeros: rows of A past M, rows of B past K.  Rows of A
+  // inside [0, M) but past this expert's count bring the next expert's data;
+  // their results are never stored.  B columns past N (edge tiles) are
+  // clamped onto the last 8 columns.  Offsets are 32-bit (the host bounds
+  // lda and ldb_k).
   int64_t r0 = row0 + m0;
   r0 = r0 < 0 ? 0 : (r0 > p.m ? p.m : r0);
   const int64_t a_end = r0 < p.m ? ((p.m - 1 - r0) * p.lda + K) * 2 : 0;
-  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(p.a + r0 * p.lda, a_end);
+  const i32x4 a_rsrc = make_rsrc4(p.a + r0 * p.lda, a_end);
   const int64_t b_end = ((K - 1) * p.ldb_k + p.n - n0) * 2;
-  const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(p.b + (int64_t)e * p.ldb_e + n0, b_end);
+  const i32x4 b_rsrc = make_rsrc4(p.b + (int64_t)e * p.ldb_e + n0, b_end);
 
-  const int a_kc = tid & 7;  // 16-byte chunk (8 K values) this thread loads
-  const uint32_t a_voff = (uint32_t)(((tid >> 3) * p.lda + a_kc * 8) * 2);
-  const uint32_t a_pass = (uint32_t)(kARowsPerPass * p.lda * 2);  // bytes between passes
-  // B: every thread loads a kBRows(k) x 8(n) block, kBRows = 8, 4, 2 for
-  // BN = 256, 128, 64, so all 256 threads take part and no load is predicated.
-  const int b_kg = tid % kKGroups;  // k group: rows kBRows*b_kg .. + kBRows-1
-  const int b_ng = tid / kKGroups;  // n group: columns 8*b_ng .. +7 of the tile
-  // Columns past N (edge tiles) are clamped onto column N-8: in bounds, and
-  // their results are never stored.
-  int64_t b_col = 8 * b_ng;
-  b_col = n0 + b_col > p.n - 8 ? p.n - 8 - n0 : b_col;
-  const uint32_t b_voff = (uint32_t)((kBRows * b_kg * p.ldb_k + b_col) * 2);
-  const uint32_t b_row = (uint32_t)(p.ldb_k * 2);
-
-  u32x4 a_reg[kAChunks];
-  u32x4 b_reg[kBRows];
-
-  // One global load of the next stage: l < kAChunks is A chunk l, else B row
-  // l - kAChunks.  A full stage (k0 + 64 <= K) has every B row and every A
-  // column in range, so the uniform stage offset rides in the SGPR offset and
-  // rows of A past M fall out of range through their VGPR offset alone.  In
-  // the partial last stage the whole offset goes through the VGPR, so the
-  // descriptor's range check zeroes A columns and B rows at k >= K.
-  auto load_one = [&](int l, int64_t k0, bool tail) {
-    if (l < kAChunks) {
-      if (!tail) {
-        a_reg[l] = bload(a_rsrc, a_voff + l * a_pass, (int)(k0 * 2));
-      } else {
-        const bool in = k0 + a_kc * 8 < K;
-        a_reg[l] = bload(a_rsrc, in ? a_voff + (uint32_t)(k0 * 2) + l * a_pass : kOutOfRange, 0);
-      }
-    } else {
-      const int r = l - kAChunks;
-      if (!tail) {
-        b_reg[r] = bload(b_rsrc, b_voff + r * b_row, (int)((uint32_t)k0 * b_row));
-      } else {
-        const bool in = k0 + kBRows * b_kg + r < K;
-        b_reg[r] = bload(b_rsrc, in ? b_voff + ((uint32_t)k0 + r) * b_row : kOutOfRange, 0);
-      }
-    }
-  };
-
-  // One LDS store of the next stage: s < kAChunks stores A chunk s; else
-  // column t = s - kAChunks of this thread's B block, transposed in registers
-  // (b_reg[q][t/2] holds columns t&~1, t|1 of k row q) into kBRows K values.
-  auto store_one = [&](int s, int buf) {
-    if (s < kAChunks) {
-      lds_store(lds_a + buf * (BM * kLdsRow), lds_off((tid >> 3) + kARowsPerPass * s, a_kc),
-                a_reg[s]);
-      return;
-    }
-    const int t = s - kAChunks;
-    const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;
-    uint32_t colv[kBRows / 2];
+  // Per-lane DMA source offsets (bytes, stage 0) and the K position of the
+  // chunk each lane moves.
+  // Chunk (row, K position) moved by lane `lane` in the t-th DMA of a stage.
+  auto a_row = [&](int t) { return 16 * (wave * kAPerWave + t) + (lane >> 2); };
+  auto a_kpos = [&](int t) { return 8 * ((lane & 3) ^ ((a_row(t) >> 2) & 3)); };
+  auto b_krow = [&](int t) { return (wave * kBPerWave + t) * kBRowsPerDma + lane / kBChunks; };
+  uint32_t a_voff[kAPerWave];
 #pragma unroll
-    for (int q = 0; q < kBRows / 2; ++q)
-      colv[q] = __builtin_amdgcn_perm(b_reg[2 * q + 1][t >> 1], b_reg[2 * q][t >> 1], sel);
-    uint8_t* dst = lds_b + buf * (BN * kLdsRow) + (8 * b_ng + t) * kLdsRow + b_kg * kBRows * 2;
-    if constexpr (kBRows == 8) {
-      *reinterpret_cast<u32x4*>(dst) = u32x4{colv[0], colv[1], colv[2], colv[3]};
-    } else if constexpr (kBRows == 4) {
-      *reinterpret_cast<u32x2*>(dst) = u32x2{colv[0], colv[1]};
+  for (int t = 0; t < kAPerWave; ++t) a_voff[t] = (uint32_t)((a_row(t) * p.lda + a_kpos(t)) * 2);
+  uint32_t b_voff[kBPerWave];
+#pragma unroll
+  for (int t = 0; t < kBPerWave; ++t) {
+    const int k = b_krow(t);
+    const int swz = BN >= 128 ? 4 * (k & 3) : 4 * ((k >> 1) & 1);
+    int64_t col = 8 * ((lane % kBChunks) ^ swz);
+    col = n0 + col > p.n - 8 ? p.n - 8 - n0 : col;
+    b_voff[t] = (uint32_t)((k * p.ldb_k + col) * 2);
+  }
+  const uint32_t b_row_bytes = (uint32_t)(p.ldb_k * 2);
+  const uint32_t lds_a0 = lds_addr(lds);
+  const uint32_t lds_b0 = lds_a0 + kStages * kAStage;
+
+  // Issues this wave's DMAs of stage s (k0 = 32 s) into LDS buffer s % 4.
+  // A full stage keeps the stage offset in the SGPR offset; the partial last
+  // stage puts it in the VGPR offset and redirects chunks at k >= K past the
+  // descriptor, which makes the DMA write zeros.
+  auto issue_stage = [&](int s) {
+    const int64_t k0 = (int64_t)s * kBK;
+    const int buf = s & (kStages - 1);
+    const uint32_t la = lds_a0 + buf * kAStage + wave * kAPerWave * 1024;
+    const uint32_t lb = lds_b0 + buf * kBStage + wave * kBPerWave * 1024;
+    if (k0 + kBK <= K) {
+#pragma unroll
+      for (int t = 0; t < kAPerWave; ++t) dma16(a_rsrc, a_voff[t], (uint32_t)(k0 * 2), la + t * 1024);
+#pragma unroll
+      for (int t = 0; t < kBPerWave; ++t)
+        dma16(b_rsrc, b_voff[t], (uint32_t)k0 * b_row_bytes, lb + t * 1024);
     } else {
-      *reinterpret_cast<uint32_t*>(dst) = colv[0];
+#pragma unroll
+      for (int t = 0; t < kAPerWave; ++t) {
+        const uint32_t v = k0 + a_kpos(t) < K ? a_voff[t] + (uint32_t)(k0 * 2) : kOutOfRange;
+        dma16(a_rsrc, v, 0u, la + t * 1024);
+      }
+#pragma unroll
+      for (int t = 0; t < kBPerWave; ++t) {
+        const uint32_t v =
+            k0 + b_krow(t) < K ? b_voff[t] + (uint32_t)k0 * b_row_bytes : kOutOfRange;
+        dma16(b_rsrc, v, 0u, lb + t * 1024);
+      }
     }
   };
+
+  // ---- fragment addresses (LDS bytes, stage 0) ----------------------------
+  const int frag_row = lane & 31;
+  const int half = lane >> 5;
+  const int a_swz = (frag_row >> 2) & 3;
+  const uint32_t a_frag0 = (uint32_t)((wm * (BM / 2) + frag_row) * 64);
+  const uint32_t a_off[2] = {lds_a0 + a_frag0 + (uint32_t)(((0 + half) ^ a_swz) * 16),
+                             lds_a0 + a_frag0 + (uint32_t)(((2 + half) ^ a_swz) * 16)};
+  const int tg = lane >> 4, ts = lane & 15;  // transposing-read group and source lane
+  const int b_row_l = 8 * (tg >> 1) + (ts >> 2);
+  const int b_swz = BN >= 128 ? 4 * ((ts >> 2) & 3) : 4 * ((ts >> 3) & 1);
+  uint32_t b_off[kNB];
+#pragma unroll
+  for (int i = 0; i < kNB; ++i) {
+    const int n = wn * (BN / 2) + 32 * i + 16 * (tg & 1) + 4 * (ts & 3);
+    b_off[i] = lds_b0 + (uint32_t)(b_row_l * kBRowBytes + (((n >> 3) ^ b_swz) * 16) + (n & 7) * 2);
+  }
 
   f32x16 acc[kNB][kMB];
 #pragma unroll
@@ -284,98 +348,92 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  const int frag_row = lane & 31;
-  const int frag_half = lane >> 5;
-  const int a_row_base = wm * (BM / 2) + frag_row;
-  const int b_row_base = wn * (BN / 2) + frag_row;
-  u32x4 fa[2][kMB];  // A fragments of two consecutive 16-wide K steps
-  u32x4 fb[2][kNB];  // B^T fragments
-  auto read_frag_a = [&](int buf, int kk, int slot, int j) {
-    fa[slot][j] = lds_load(lds_a + buf * (BM * kLdsRow),
-                           lds_off(a_row_base + 32 * j, 2 * kk + frag_half));
+  u32x4 fa[2][kMB];  // A fragments of the stage's two 16-wide K steps
+  u32x4 fb[2][kNB];  // B fragments
+  auto read_a = [&](int buf, int kk, int j) {
+    fa[kk][j] = lds_load(lds, a_off[kk] + buf * kAStage + 2048 * j - lds_a0);
   };
-  auto read_frag_b = [&](int buf, int kk, int slot, int i) {
-    fb[slot][i] = lds_load(lds_b + buf * (BN * kLdsRow),
-                           lds_off(b_row_base + 32 * i, 2 * kk + frag_half));
+  auto read_b = [&](int buf, int kk, int i) {
+    const uint32_t base = b_off[i] + buf * kBStage + 16 * kk * kBRowBytes - lds_a0;
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_i16x4*)(lds_ptr(lds) + base));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_i16x4*)(lds_ptr(lds) + base + 4 * kBRowBytes));
+    const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
+    const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
+    fb[kk][i] = u32x4{l2[0], l2[1], h2[0], h2[1]};
   };
-
-  // One K stage in explicit program order.  The stage's 4 K steps x 4 groups
-  // each issue a quarter of the K step's MFMAs followed by (a) a quarter of
-  // the next K step's fragment reads, (b) in the first 8 groups, 1/8 of the
-  // next stage's global loads, (c) in the last 8 groups, 1/8 of its
-  // transposes and LDS stores.  sched_barrier fences keep this order: a wave
-  // issues in order, so a burst of loads would stall its MFMAs behind a full
-  // memory queue, and fragment reads issued late would stall each MFMA.
-  // Fragments of K step 0 must already be in fa[0]/fb[0].
-  constexpr int kMfmaPerStep = kMB * kNB;
-  constexpr int kLoads = kAChunks + kBRows;
-  constexpr int kStores = kAChunks + 8;
-  auto stage = [&](int buf, int nbuf, int64_t k0_next, bool load_next, bool tail_next) {
+  auto read_kstep = [&](int buf, int kk, int g) {  // quarter g of a K step's fragments
 #pragma unroll
-    for (int kk = 0; kk < kBK / 16; ++kk) {
-      const int cur = kk & 1;
+    for (int j = g; j < kMB; j += 4) read_a(buf, kk, j);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
+    for (int i = g; i < kNB; i += 4) read_b(buf, kk, i);
+  };
+  auto mfma_group = [&](int kk, int g) {  // quarter g of a K step's MFMAs
+    constexpr int kPer = kMB * kNB;
 #pragma unroll
-        for (int p = g * kMfmaPerStep / 4; p < (g + 1) * kMfmaPerStep / 4; ++p) {
-          const int i = p / kMB, j = p % kMB;
-          acc[i][j] = T::mfma(fb[cur][i], fa[cur][j], acc[i][j]);
-        }
-        if (kk + 1 < kBK / 16) {
-#pragma unroll
-          for (int j = g; j < kMB; j += 4) read_frag_a(buf, kk + 1, cur ^ 1, j);
-#pragma unroll
-          for (int i = g; i < kNB; i += 4) read_frag_b(buf, kk + 1, cur ^ 1, i);
-        }
-        if (load_next) {
-          const int grp = kk * 4 + g;  // 0..15
-          if (grp < 8) {
-#pragma unroll
-            for (int l = grp * kLoads / 8; l < (grp + 1) * kLoads / 8; ++l)
-              load_one(l, k0_next, tail_next);
-          } else {
-#pragma unroll
-            for (int t = (grp - 8) * kStores / 8; t < (grp - 7) * kStores / 8; ++t)
-              store_one(t, nbuf);
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    for (int q = g * kPer / 4; q < (g + 1) * kPer / 4; ++q) {
+      const int i = q / kMB, j = q % kMB;
+      acc[i][j] = T::mfma(fb[kk][i], fa[kk][j], acc[i][j]);
     }
   };
-  auto first_frags = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < kMB; ++j) read_frag_a(buf, 0, 0, j);
-#pragma unroll
-    for (int i = 0; i < kNB; ++i) read_frag_b(buf, 0, 0, i);
-  };
 
-  // Stage pipeline: stage kt computes from LDS buffer kt&1 while the next
-  // stage moves global -> registers -> LDS buffer (kt+1)&1; one barrier per
-  // stage.
   const int nk = (int)((K + kBK - 1) / kBK);
-  const int nk_full = (int)(K / kBK);  // stages with k0 + 64 <= K
-#pragma unroll
-  for (int l = 0; l < kLoads; ++l) load_one(l, 0, nk_full == 0);
-  __syncthreads();  // the previous tile's waves are done with the LDS stages
-#pragma unroll
-  for (int t = 0; t < kStores; ++t) store_one(t, 0);
+  __syncthreads();  // the previous tile's waves are done reading the LDS stages
+  // Prologue: stages 0..2 in flight, wait for stage 0.
+  if (nk > 0) issue_stage(0);
+  if (nk > 1) issue_stage(1);
+  if (nk > 2) issue_stage(2);
+  if (nk > 2) wait_dma<2 * kDmaPerStage>();
+  else if (nk > 1) wait_dma<kDmaPerStage>();
+  else wait_dma<0>();
   __syncthreads();
-  int kt = 0;
-  for (; kt + 1 < nk_full; ++kt) {
-    first_frags(kt & 1);
-    stage(kt & 1, (kt + 1) & 1, (int64_t)(kt + 1) * kBK, true, false);
-    __syncthreads();
-  }
-  if (kt + 1 < nk) {  // the partial last stage when K % 64 != 0
-    first_frags(kt & 1);
-    stage(kt & 1, (kt + 1) & 1, (int64_t)(kt + 1) * kBK, true, true);
-    __syncthreads();
-    ++kt;
-  }
   if (nk > 0) {
-    first_frags(kt & 1);
-    stage(kt & 1, 0, 0, false, false);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) read_kstep(0, 0, g);
+  }
+
+  // K step 0 of a stage: MFMAs with the fragments of K step 1 read in between.
+  auto kstep0 = [&](int buf) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      mfma_group(0, g);
+      read_kstep(buf, 1, g);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // Steady state: every stage but the last has a successor to publish.
+  int kt = 0;
+  for (; kt + 1 < nk; ++kt) {
+    const int buf = kt & (kStages - 1);
+    // Stage kt+3 goes into the buffer stage kt-1 used; every wave finished
+    // reading it before the barrier of stage kt-1.
+    if (kt + 3 < nk) issue_stage(kt + 3);
+    kstep0(buf);
+    mfma_group(1, 0);
+    mfma_group(1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    // Publish stage kt+1: this wave's DMAs of it are done once at most the
+    // DMAs of the (up to two) later stages are outstanding.
+    if (kt + 3 < nk) wait_dma<2 * kDmaPerStage>();
+    else if (kt + 2 < nk) wait_dma<kDmaPerStage>();
+    else wait_dma<0>();
+    __syncthreads();
+    // Its first fragments load while the last MFMAs of this stage run.
+    const int nbuf = (kt + 1) & (kStages - 1);
+    mfma_group(1, 2);
+    read_kstep(nbuf, 0, 0);
+    read_kstep(nbuf, 0, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_group(1, 3);
+    read_kstep(nbuf, 0, 2);
+    read_kstep(nbuf, 0, 3);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (nk > 0) {  // the last stage
+    kstep0(kt & (kStages - 1));
+#pragma unroll
+    for (int g = 0; g < 4; ++g) mfma_group(1, g);
   }
 
   // ---- epilogue: acc[i][j] register r holds D[n][m] of the 32x32 block with
@@ -391,7 +449,7 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
     for (int i = 0; i < kNB; ++i) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int64_t n = n0 + wn * (BN / 2) + 32 * i + 8 * g + 4 * frag_half;
+        const int64_t n = n0 + wn * (BN / 2) + 32 * i + 8 * g + 4 * half;
         if (row_ok && n < p.n) {
           u32x2 v;
           v[0] = T::pack(acc[i][j][4 * g + 0], acc[i][j][4 * g + 1]);
@@ -403,12 +461,16 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   }
 }
 
+template <int BM, int BN>
+constexpr int lds_bytes() {
+  return 4 * (BM + BN) * 32 * 2;
+}
+
 template <int BM, int BN, class T>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(1, 1))) void
 grouped_gemm_kernel(GemmParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds_a[2 * BM * kLdsRow];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_b[2 * BN * kLdsRow];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes<BM, BN>()];
   __shared__ int32_t s_prefix[kMaxLdsExpertsGemm + 1];
   __shared__ int32_t s_scan[kThreads];
   __shared__ int32_t s_item;
@@ -440,7 +502,7 @@ grouped_gemm_kernel(GemmParams p) {
   };
   int32_t w = p.atomic ? next_ticket() : v;
   while ((uint32_t)w < (uint32_t)W) {
-    run_tile<BM, BN, T>(p, w, n_tiles, s_prefix, lds_a, lds_b);
+    run_tile<BM, BN, T>(p, w, n_tiles, s_prefix, lds);
     w = p.atomic ? next_ticket() : w + G;
   }
   if (!p.atomic) return;
