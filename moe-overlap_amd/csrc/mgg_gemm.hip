@@ -30,6 +30,14 @@
 #include "mgg.h"
 #include "mgg_internal.h"
 
+#ifndef MGG_SBK256
+#define MGG_SBK256 64
+#define MGG_NS256 2
+#endif
+#ifndef MGG_NW256
+#define MGG_NW256 8
+#endif
+
 namespace mgg {
 namespace {
 
@@ -102,12 +110,12 @@ __device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t rsrc, uint32_t vof
 // workgroup: prefix[e] = sum_{j<e} ceil(max(off[j+1]-off[j],0)/BM) * n_tiles.
 // Returns the queue length W = prefix[E].  Same counts as
 // src/triton_grouped_gemm.py:253-271.
-template <int BM>
+template <int BM, int NT>
 __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_prefix,
                                  int32_t* s_scan) {
   const int tid = threadIdx.x;
   const int E = p.num_experts;
-  const int per = (E + kThreads - 1) / kThreads;
+  const int per = (E + NT - 1) / NT;
   const int e0 = tid * per;
   int32_t local = 0;
   for (int i = 0; i < per; ++i) {
@@ -120,8 +128,8 @@ __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_pr
   }
   s_scan[tid] = local;
   __syncthreads();
-  // Hillis-Steele inclusive scan over the 256 per-thread sums.
-  for (int d = 1; d < kThreads; d <<= 1) {
+  // Hillis-Steele inclusive scan over the NT per-thread sums.
+  for (int d = 1; d < NT; d <<= 1) {
     const int32_t add = tid >= d ? s_scan[tid - d] : 0;
     __syncthreads();
     s_scan[tid] += add;
@@ -136,7 +144,7 @@ __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_pr
       base += cnt > 0 ? (int32_t)(((cnt + BM - 1) / BM) * (int64_t)n_tiles) : 0;
     }
   }
-  if (tid == kThreads - 1) s_prefix[E] = s_scan[kThreads - 1];
+  if (tid == NT - 1) s_prefix[E] = s_scan[NT - 1];
   __syncthreads();
   return s_prefix[E];
 }
@@ -145,9 +153,9 @@ __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_pr
 __device__ void zero_fill(const GemmParams& p) {
   const int64_t chunks_per_row = p.n / 8;
   const int64_t total = p.m * chunks_per_row;
-  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const u32x4 z = {0u, 0u, 0u, 0u};
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total; i += stride) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
     const int64_t r = i / chunks_per_row;
     const int64_t c8 = i - r * chunks_per_row;
     *reinterpret_cast<u32x4*>(p.c + r * p.ldc + c8 * 8) = z;
@@ -179,9 +187,9 @@ __device__ __forceinline__ i32x4 make_rsrc4(const void* base, int64_t bytes) {
   const int64_t cap = 0x7FFFFFF0LL;
   const uint64_t addr = reinterpret_cast<uint64_t>(base);
   i32x4 r;
-  r[0] = (int32_t)(uint32_t)addr;
-  r[1] = (int32_t)(uint32_t)((addr >> 32) & 0xFFFFu);  // stride 0
-  r[2] = (int32_t)(bytes < 0 ? 0 : (bytes > cap ? cap : bytes));
+  r[0] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)addr);
+  r[1] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)((addr >> 32) & 0xFFFFu));  // stride 0
+  r[2] = __builtin_amdgcn_readfirstlane((int32_t)(bytes < 0 ? 0 : (bytes > cap ? cap : bytes)));
   r[3] = 0x00020000;  // gfx9-family default format
   return r;
 }
@@ -193,34 +201,45 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // Computes one output tile.  All arguments are uniform across the workgroup,
 // so the early returns never split a barrier.
 //
-// K advances in stages of 32; four stages rotate through LDS.  A stage holds
-// A [BM x 32] as BM rows of 64 bytes and B [32 x BN] in its global layout
-// (K rows of BN contiguous N values); both arrive by DMA, three stages ahead
-// of the one being multiplied.  16-byte chunks are XOR-swizzled on the global
-// side so that the fragment reads below are bank-conflict free:
-//   A row r, chunk c  -> physical chunk c ^ ((r >> 2) & 3)
-//   B row k, chunk c  -> physical chunk c ^ 4*(k & 3)        (BN >= 128)
-//                                        c ^ 4*((k >> 1) & 1) (BN == 64)
+// K advances in stages of SBK (32 or 64); NSTAGE stages rotate through LDS.
+// A stage holds A [BM x SBK] as BM rows of 2*SBK bytes and B [SBK x BN] in
+// its global layout (K rows of BN contiguous N values); both arrive by DMA,
+// NSTAGE-1 stages ahead of the one being multiplied.  16-byte chunks are
+// XOR-swizzled on the global side so that the fragment reads below are
+// bank-conflict free:
+//   A row r, chunk c  -> physical chunk c ^ ((r >> 2) & 3)    (SBK == 32)
+//                                        c ^ ((r >> 1) & 7)    (SBK == 64)
+//   B row k, chunk c  -> physical chunk c ^ 4*(k & 3)          (BN >= 128)
+//                                        c ^ 4*((k >> 1) & 1)  (BN == 64)
 // A fragments are ds_read_b128 (8 consecutive K of one row).  B fragments use
 // the gfx950 transposing read ds_read_b64_tr_b16: in each group of 16 lanes,
 // lane s addresses B[k0 + s/4][n0 + 4*(s%4) .. +3] and lane j receives
 // B[k0 .. k0+3][n0 + j], so two reads give a lane the 8 consecutive K of its
 // column that the MFMA expects.
-template <int BM, int BN, class T>
+template <int BM, int BN, int SBK, int NSTAGE, int NW, class T>
 __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int n_tiles,
                                          const int32_t* s_prefix, uint8_t* lds) {
-  constexpr int kBK = 32;                   // K per stage
-  constexpr int kStages = 4;                // LDS stages in rotation
-  constexpr int kAStage = BM * kBK * 2;     // bytes of A per stage
+  constexpr int kBK = SBK;                  // K per stage
+  constexpr int kStages = NSTAGE;           // LDS stages in rotation
+  constexpr int kSteps = kBK / 16;          // MFMA K steps per stage
+  constexpr int kARowBytes = kBK * 2;
+  constexpr int kAChunks = kBK / 8;         // 16-byte chunks per A row
+  constexpr int kARowsPerDma = 64 / kAChunks;
+  constexpr int kAStage = BM * kARowBytes;  // bytes of A per stage
   constexpr int kBStage = kBK * BN * 2;     // bytes of B per stage
   constexpr int kBRowBytes = BN * 2;
-  constexpr int kAPerWave = BM / 64;        // A DMAs per wave per stage (16 rows each)
-  constexpr int kBPerWave = BN / 64;        // B DMAs per wave per stage
+  constexpr int kAPerWave = BM / (NW * kARowsPerDma);  // A DMAs per wave per stage
+  constexpr int kBPerWave = kBStage / (1024 * NW);     // B DMAs per wave per stage
+  constexpr int kWN = NW / 2;                          // waves along N (2 along M)
+  static_assert(kAPerWave >= 1 && kBPerWave >= 1, "tile too small for the wave count");
+  static_assert(kSteps == 2 || kSteps == 4, "K per stage must be 32 or 64");
+  static_assert(kStages >= 2, "need at least two LDS stages");
   constexpr int kDmaPerStage = kAPerWave + kBPerWave;
   constexpr int kBChunks = BN / 8;          // 16-byte chunks per B row
   constexpr int kBRowsPerDma = 64 / kBChunks;
   constexpr int kMB = BM / 64;              // 32-row MFMA blocks per wave
-  constexpr int kNB = BN / 64;              // 32-col MFMA blocks per wave
+  constexpr int kNB = BN / (32 * kWN);      // 32-col MFMA blocks per wave
+  static_assert(kNB >= 1, "tile too narrow for the wave count");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -246,6 +265,11 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
     tm = local / n_tiles;
     tn = local - tm * n_tiles;
   }
+  // Uniform across the workgroup (LDS reads look divergent to the compiler):
+  // keep the tile coordinates, and everything derived from them, in SGPRs.
+  e = __builtin_amdgcn_readfirstlane(e);
+  tm = __builtin_amdgcn_readfirstlane(tm);
+  tn = __builtin_amdgcn_readfirstlane(tn);
 
   const int64_t row0 = p.offsets[e];
   const int64_t cnt = (int64_t)p.offsets[e + 1] - row0;
@@ -274,8 +298,9 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   // Per-lane DMA source offsets (bytes, stage 0) and the K position of the
   // chunk each lane moves.
   // Chunk (row, K position) moved by lane `lane` in the t-th DMA of a stage.
-  auto a_row = [&](int t) { return 16 * (wave * kAPerWave + t) + (lane >> 2); };
-  auto a_kpos = [&](int t) { return 8 * ((lane & 3) ^ ((a_row(t) >> 2) & 3)); };
+  auto a_swz = [](int r) { return kAChunks == 4 ? (r >> 2) & 3 : (r >> 1) & 7; };
+  auto a_row = [&](int t) { return kARowsPerDma * (wave * kAPerWave + t) + lane / kAChunks; };
+  auto a_kpos = [&](int t) { return 8 * ((lane % kAChunks) ^ a_swz(a_row(t))); };
   auto b_krow = [&](int t) { return (wave * kBPerWave + t) * kBRowsPerDma + lane / kBChunks; };
   uint32_t a_voff[kAPerWave];
 #pragma unroll
@@ -293,50 +318,56 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   const uint32_t lds_a0 = lds_addr(lds);
   const uint32_t lds_b0 = lds_a0 + kStages * kAStage;
 
-  // Issues this wave's DMAs of stage s (k0 = 32 s) into LDS buffer s % 4.
-  // A full stage keeps the stage offset in the SGPR offset; the partial last
-  // stage puts it in the VGPR offset and redirects chunks at k >= K past the
+  // Issues DMAs [d0, d1) of this wave's kDmaPerStage DMAs of stage s (the
+  // first kAPerWave move A, the rest B) into LDS buffer s % kStages.  A full
+  // stage keeps the stage offset in the SGPR offset; the partial last stage
+  // puts it in the VGPR offset and redirects chunks at k >= K past the
   // descriptor, which makes the DMA write zeros.
-  auto issue_stage = [&](int s) {
+  auto issue_part = [&](int s, int d0, int d1) {
     const int64_t k0 = (int64_t)s * kBK;
-    const int buf = s & (kStages - 1);
+    const int buf = s % kStages;
     const uint32_t la = lds_a0 + buf * kAStage + wave * kAPerWave * 1024;
     const uint32_t lb = lds_b0 + buf * kBStage + wave * kBPerWave * 1024;
-    if (k0 + kBK <= K) {
+    const bool full = k0 + kBK <= K;
 #pragma unroll
-      for (int t = 0; t < kAPerWave; ++t) dma16(a_rsrc, a_voff[t], (uint32_t)(k0 * 2), la + t * 1024);
-#pragma unroll
-      for (int t = 0; t < kBPerWave; ++t)
-        dma16(b_rsrc, b_voff[t], (uint32_t)k0 * b_row_bytes, lb + t * 1024);
-    } else {
-#pragma unroll
-      for (int t = 0; t < kAPerWave; ++t) {
-        const uint32_t v = k0 + a_kpos(t) < K ? a_voff[t] + (uint32_t)(k0 * 2) : kOutOfRange;
-        dma16(a_rsrc, v, 0u, la + t * 1024);
-      }
-#pragma unroll
-      for (int t = 0; t < kBPerWave; ++t) {
-        const uint32_t v =
-            k0 + b_krow(t) < K ? b_voff[t] + (uint32_t)k0 * b_row_bytes : kOutOfRange;
-        dma16(b_rsrc, v, 0u, lb + t * 1024);
+    for (int d = d0; d < d1; ++d) {
+      if (d < kAPerWave) {
+        const int t = d;
+        if (full) {
+          dma16(a_rsrc, a_voff[t], (uint32_t)(k0 * 2), la + t * 1024);
+        } else {
+          const uint32_t v = k0 + a_kpos(t) < K ? a_voff[t] + (uint32_t)(k0 * 2) : kOutOfRange;
+          dma16(a_rsrc, v, 0u, la + t * 1024);
+        }
+      } else {
+        const int t = d - kAPerWave;
+        if (full) {
+          dma16(b_rsrc, b_voff[t], (uint32_t)k0 * b_row_bytes, lb + t * 1024);
+        } else {
+          const uint32_t v =
+              k0 + b_krow(t) < K ? b_voff[t] + (uint32_t)k0 * b_row_bytes : kOutOfRange;
+          dma16(b_rsrc, v, 0u, lb + t * 1024);
+        }
       }
     }
   };
+  auto issue_stage = [&](int s) { issue_part(s, 0, kDmaPerStage); };
 
   // ---- fragment addresses (LDS bytes, stage 0) ----------------------------
   const int frag_row = lane & 31;
   const int half = lane >> 5;
-  const int a_swz = (frag_row >> 2) & 3;
-  const uint32_t a_frag0 = (uint32_t)((wm * (BM / 2) + frag_row) * 64);
-  const uint32_t a_off[2] = {lds_a0 + a_frag0 + (uint32_t)(((0 + half) ^ a_swz) * 16),
-                             lds_a0 + a_frag0 + (uint32_t)(((2 + half) ^ a_swz) * 16)};
+  const uint32_t a_frag0 = (uint32_t)((wm * (BM / 2) + frag_row) * kARowBytes);
+  uint32_t a_off[kSteps];  // rows 32j further are +32j*kARowBytes (same swizzle)
+#pragma unroll
+  for (int kk = 0; kk < kSteps; ++kk)
+    a_off[kk] = lds_a0 + a_frag0 + (uint32_t)(((2 * kk + half) ^ a_swz(frag_row)) * 16);
   const int tg = lane >> 4, ts = lane & 15;  // transposing-read group and source lane
   const int b_row_l = 8 * (tg >> 1) + (ts >> 2);
   const int b_swz = BN >= 128 ? 4 * ((ts >> 2) & 3) : 4 * ((ts >> 3) & 1);
   uint32_t b_off[kNB];
 #pragma unroll
   for (int i = 0; i < kNB; ++i) {
-    const int n = wn * (BN / 2) + 32 * i + 16 * (tg & 1) + 4 * (ts & 3);
+    const int n = wn * (BN / kWN) + 32 * i + 16 * (tg & 1) + 4 * (ts & 3);
     b_off[i] = lds_b0 + (uint32_t)(b_row_l * kBRowBytes + (((n >> 3) ^ b_swz) * 16) + (n & 7) * 2);
   }
 
@@ -348,10 +379,10 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  u32x4 fa[2][kMB];  // A fragments of the stage's two 16-wide K steps
+  u32x4 fa[2][kMB];  // A fragments of two consecutive 16-wide K steps
   u32x4 fb[2][kNB];  // B fragments
   auto read_a = [&](int buf, int kk, int j) {
-    fa[kk][j] = lds_load(lds, a_off[kk] + buf * kAStage + 2048 * j - lds_a0);
+    fa[kk & 1][j] = lds_load(lds, a_off[kk] + buf * kAStage + 32 * kARowBytes * j - lds_a0);
   };
   auto read_b = [&](int buf, int kk, int i) {
     const uint32_t base = b_off[i] + buf * kBStage + 16 * kk * kBRowBytes - lds_a0;
@@ -361,79 +392,103 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
         (lds_i16x4*)(lds_ptr(lds) + base + 4 * kBRowBytes));
     const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
     const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
-    fb[kk][i] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+    fb[kk & 1][i] = u32x4{l2[0], l2[1], h2[0], h2[1]};
   };
-  auto read_kstep = [&](int buf, int kk, int g) {  // quarter g of a K step's fragments
+  auto read_kstep = [&](int buf, int kk, int part) {  // half `part` of a K step's fragments
 #pragma unroll
-    for (int j = g; j < kMB; j += 4) read_a(buf, kk, j);
+    for (int j = part * kMB / 2; j < (part + 1) * kMB / 2 + (kMB == 1 && part == 0); ++j)
+      read_a(buf, kk, j);
 #pragma unroll
-    for (int i = g; i < kNB; i += 4) read_b(buf, kk, i);
+    for (int i = part * kNB / 2; i < (part + 1) * kNB / 2 + (kNB == 1 && part == 0); ++i)
+      read_b(buf, kk, i);
   };
   auto mfma_group = [&](int kk, int g) {  // quarter g of a K step's MFMAs
     constexpr int kPer = kMB * kNB;
 #pragma unroll
     for (int q = g * kPer / 4; q < (g + 1) * kPer / 4; ++q) {
       const int i = q / kMB, j = q % kMB;
-      acc[i][j] = T::mfma(fb[kk][i], fa[kk][j], acc[i][j]);
+      acc[i][j] = T::mfma(fb[kk & 1][i], fa[kk & 1][j], acc[i][j]);
     }
+  };
+
+  // Waits until this wave's DMAs of every stage up to `s` are complete, given
+  // that stages up to `last_issued` have been issued (each stage is
+  // kDmaPerStage DMAs, and DMAs complete in issue order).
+  auto wait_stage = [&](int s, int last_issued) {
+    const int later = last_issued - s;  // 0 .. kStages-2
+    if (kStages > 3 && later >= 3) wait_dma<3 * kDmaPerStage>();
+    else if (kStages > 2 && later == 2) wait_dma<2 * kDmaPerStage>();
+    else if (later == 1) wait_dma<kDmaPerStage>();
+    else wait_dma<0>();
   };
 
   const int nk = (int)((K + kBK - 1) / kBK);
   __syncthreads();  // the previous tile's waves are done reading the LDS stages
-  // Prologue: stages 0..2 in flight, wait for stage 0.
-  if (nk > 0) issue_stage(0);
-  if (nk > 1) issue_stage(1);
-  if (nk > 2) issue_stage(2);
-  if (nk > 2) wait_dma<2 * kDmaPerStage>();
-  else if (nk > 1) wait_dma<kDmaPerStage>();
-  else wait_dma<0>();
+  // Prologue: stages 0 .. kStages-2 in flight, wait for stage 0.
+  int issued = -1;
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s)
+    if (s < nk) issue_stage(issued = s);
+  wait_stage(0, issued);
   __syncthreads();
   if (nk > 0) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) read_kstep(0, 0, g);
+    read_kstep(0, 0, 0);
+    read_kstep(0, 0, 1);
   }
 
-  // K step 0 of a stage: MFMAs with the fragments of K step 1 read in between.
-  auto kstep0 = [&](int buf) {
+  // MFMA groups of a stage in program order.  Each K step's 4 groups are
+  // followed by: the next K step's fragment reads (half after group 0, half
+  // after group 1, so they have two groups of MFMAs to land), and a share of
+  // the DMAs of stage kt+kStages-1 (spread over the early groups so a wave
+  // never stalls behind a burst of them).  In the last K step the barrier
+  // that publishes stage kt+1 comes after group 0 (by then every fragment of
+  // this stage has been read), and stage kt+1's first fragments are read
+  // after groups 1 and 2.
+  constexpr int kEarlyGroups = 4 * (kSteps - 1);
+  auto dma_share = [&](int grp, int s) {
+    const int d0 = grp * kDmaPerStage / kEarlyGroups;
+    const int d1 = (grp + 1) * kDmaPerStage / kEarlyGroups;
+    if (d1 > d0) issue_part(s, d0, d1);
+  };
+  auto early_steps = [&](int buf, int next_stage, bool issue) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      mfma_group(0, g);
-      read_kstep(buf, 1, g);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int kk = 0; kk + 1 < kSteps; ++kk) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        mfma_group(kk, g);
+        if (g < 2) read_kstep(buf, kk + 1, g);
+        if (issue) dma_share(kk * 4 + g, next_stage);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   };
   // Steady state: every stage but the last has a successor to publish.
   int kt = 0;
   for (; kt + 1 < nk; ++kt) {
-    const int buf = kt & (kStages - 1);
-    // Stage kt+3 goes into the buffer stage kt-1 used; every wave finished
-    // reading it before the barrier of stage kt-1.
-    if (kt + 3 < nk) issue_stage(kt + 3);
-    kstep0(buf);
-    mfma_group(1, 0);
-    mfma_group(1, 1);
+    const int buf = kt % kStages;
+    // Stage kt+kStages-1 goes into the buffer stage kt-1 used; every wave
+    // finished reading it before the barrier of stage kt-1.
+    const bool issue = kt + kStages - 1 < nk;
+    if (issue) issued = kt + kStages - 1;
+    early_steps(buf, kt + kStages - 1, issue);
+    mfma_group(kSteps - 1, 0);
     __builtin_amdgcn_sched_barrier(0);
-    // Publish stage kt+1: this wave's DMAs of it are done once at most the
-    // DMAs of the (up to two) later stages are outstanding.
-    if (kt + 3 < nk) wait_dma<2 * kDmaPerStage>();
-    else if (kt + 2 < nk) wait_dma<kDmaPerStage>();
-    else wait_dma<0>();
+    wait_stage(kt + 1, issued);
     __syncthreads();
-    // Its first fragments load while the last MFMAs of this stage run.
-    const int nbuf = (kt + 1) & (kStages - 1);
-    mfma_group(1, 2);
+    const int nbuf = (kt + 1) % kStages;
+    mfma_group(kSteps - 1, 1);
     read_kstep(nbuf, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_group(kSteps - 1, 2);
     read_kstep(nbuf, 0, 1);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_group(1, 3);
-    read_kstep(nbuf, 0, 2);
-    read_kstep(nbuf, 0, 3);
+    mfma_group(kSteps - 1, 3);
     __builtin_amdgcn_sched_barrier(0);
   }
   if (nk > 0) {  // the last stage
-    kstep0(kt & (kStages - 1));
+    early_steps(kt % kStages, 0, false);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) mfma_group(1, g);
+    for (int g = 0; g < 4; ++g) mfma_group(kSteps - 1, g);
   }
 
   // ---- epilogue: acc[i][j] register r holds D[n][m] of the 32x32 block with
@@ -449,7 +504,7 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
     for (int i = 0; i < kNB; ++i) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int64_t n = n0 + wn * (BN / 2) + 32 * i + 8 * g + 4 * half;
+        const int64_t n = n0 + wn * (BN / kWN) + 32 * i + 8 * g + 4 * half;
         if (row_ok && n < p.n) {
           u32x2 v;
           v[0] = T::pack(acc[i][j][4 * g + 0], acc[i][j][4 * g + 1]);
@@ -461,25 +516,31 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int SBK, int NSTAGE>
 constexpr int lds_bytes() {
-  return 4 * (BM + BN) * 32 * 2;
+  return NSTAGE * (BM + BN) * SBK * 2;
 }
 
-template <int BM, int BN, class T>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
-                          amdgpu_waves_per_eu(1, 1))) void
+// NW waves per workgroup (4: one per SIMD; 8: two per SIMD, so one wave's
+// memory and barrier stalls are filled by the other's MFMAs).  Waves form a
+// 2 x NW/2 grid over the tile.
+template <int BM, int BN, int SBK, int NSTAGE, int NW, class T>
+__global__ __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64),
+                          amdgpu_waves_per_eu(NW / 4, NW / 4))) void
 grouped_gemm_kernel(GemmParams p) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes<BM, BN>()];
+  static_assert(lds_bytes<BM, BN, SBK, NSTAGE>() <= 144 * 1024, "LDS stages exceed the budget");
+  constexpr int NT = NW * 64;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes<BM, BN, SBK, NSTAGE>()];
   __shared__ int32_t s_prefix[kMaxLdsExpertsGemm + 1];
-  __shared__ int32_t s_scan[kThreads];
+  __shared__ int32_t s_scan[NT];
   __shared__ int32_t s_item;
 
   const int tid = threadIdx.x;
   const int G = gridDim.x;
   const int n_tiles = (int)((p.n + BN - 1) / BN);
 
-  const int32_t W = p.num_work >= 0 ? p.num_work : derive_prefix<BM>(p, n_tiles, s_prefix, s_scan);
+  const int32_t W =
+      p.num_work >= 0 ? p.num_work : derive_prefix<BM, NT>(p, n_tiles, s_prefix, s_scan);
   if (W == 0) {
     zero_fill(p);
     return;
@@ -502,7 +563,7 @@ grouped_gemm_kernel(GemmParams p) {
   };
   int32_t w = p.atomic ? next_ticket() : v;
   while ((uint32_t)w < (uint32_t)W) {
-    run_tile<BM, BN, T>(p, w, n_tiles, s_prefix, lds);
+    run_tile<BM, BN, SBK, NSTAGE, NW, T>(p, w, n_tiles, s_prefix, lds);
     w = p.atomic ? next_ticket() : w + G;
   }
   if (!p.atomic) return;
@@ -525,21 +586,23 @@ __global__ void zero_i32_kernel(int32_t* ptr, int count) {
 
 template <class T>
 int launch_typed(int block_m, int block_n, const GemmParams& p, int workers, hipStream_t stream) {
-#define MGG_CASE(BM_, BN_)                                                                  \
-  if (block_m == BM_ && block_n == BN_) {                                                  \
-    hipLaunchKernelGGL((grouped_gemm_kernel<BM_, BN_, T>), dim3(workers), dim3(kThreads), 0, \
-                       stream, p);                                                         \
-    return MGG_OK;                                                                          \
+#define MGG_CASE(BM_, BN_, SBK_, NS_, NW_)                                                 \
+  if (block_m == BM_ && block_n == BN_) {                                                 \
+    hipLaunchKernelGGL((grouped_gemm_kernel<BM_, BN_, SBK_, NS_, NW_, T>), dim3(workers), \
+                       dim3(NW_ * 64), 0, stream, p);                                      \
+    return MGG_OK;                                                                         \
   }
-  MGG_CASE(256, 256)
-  MGG_CASE(256, 128)
-  MGG_CASE(128, 256)
-  MGG_CASE(128, 128)
-  MGG_CASE(128, 64)
-  MGG_CASE(64, 128)
-  MGG_CASE(64, 64)
-  MGG_CASE(256, 64)
-  MGG_CASE(64, 256)
+  // (tile, K per stage, LDS stages, waves): 128-byte A rows (64-wide K
+  // stages), as many stages as the LDS budget holds.
+  MGG_CASE(256, 256, MGG_SBK256, MGG_NS256, MGG_NW256)
+  MGG_CASE(256, 128, 64, 3, 4)
+  MGG_CASE(128, 256, 64, 3, 4)
+  MGG_CASE(128, 128, 64, 4, 4)
+  MGG_CASE(128, 64, 64, 4, 4)
+  MGG_CASE(64, 128, 64, 4, 4)
+  MGG_CASE(64, 64, 64, 4, 4)
+  MGG_CASE(256, 64, 64, 3, 4)
+  MGG_CASE(64, 256, 64, 3, 4)
 #undef MGG_CASE
   return set_error(MGG_ERR_UNSUPPORTED, "block_m/block_n must each be one of 64, 128, 256");
 }
