@@ -32,7 +32,7 @@ sys.path.insert(0, str(REPO))
 METRIC = "grouped GEMM TFLOP/s + % bf16 MFMA peak, E=16 512 tok/expert K2048 N4096"
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0
-KERNEL_NAME = "grouped_gemm_kernel<256,256,Bf16>"
+KERNEL_NAME = "grouped_gemm_kernel<256,256,64,2,8,Bf16>"
 
 
 def parse_args():
@@ -72,6 +72,21 @@ def event_times_ms(fn, iters, flush=None):
         times.append((s, e))
     torch.cuda.synchronize()
     return [s.elapsed_time(e) for s, e in times]
+
+
+PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_256x256_bf16_uniform.md"
+
+
+def recorded_traffic(mode, workload, block_m, block_n):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+    (calibrated against a plain copy), when it covers this configuration; else None."""
+    if workload != "uniform" or (block_m, block_n) != (256, 256) or not PROFILE_SUMMARY.exists():
+        return None
+    key = f"traffic_bytes_per_launch_{mode}:"
+    for line in PROFILE_SUMMARY.read_text().splitlines():
+        if line.startswith(key):
+            return int(line.split(":", 1)[1])
+    return None
 
 
 def median(xs):
@@ -243,7 +258,9 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": recorded_traffic(args.mode, args.workload, args.block_m, args.block_n),
+            "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), "
+                              "profiles/grouped_gemm_256x256_bf16_uniform.md",
             "kernel": KERNEL_NAME if (args.block_m, args.block_n) == (256, 256) else "grouped_gemm_kernel",
             "algorithmic_flops_per_launch": flops,
             "algorithmic_bytes_per_launch": case.algorithmic_bytes(),

@@ -1,6 +1,6 @@
 // Persistent expert-grouped GEMM for gfx950 (MI355X).
 //
-// One workgroup of 256 threads (4 wave64s) per CU walks a queue of
+// A persistent grid (one workgroup per CU by default) walks a queue of
 // BLOCK_M x BLOCK_N output tiles (expert-major, then tile_m, then tile_n, the
 // order of src/triton_grouped_gemm.py:277-292).  Workers either stride over
 // the queue (the striped kernel, :101-154) or dequeue with a global atomic
@@ -8,25 +8,13 @@
 // A[off_e + tm*BM + i, k] * B[e, k, tn*BN + j] (:36-98): rows past the expert's
 // count are never stored, fp32 accumulation, output rounded to the input type.
 //
-// Data path per 64-wide K stage:
-//   * A [BM x 64] moves HBM -> registers with 16-byte loads (8 lanes cover one
-//     128-byte row segment) and is written to LDS row-major, K contiguous.
-//   * B is stored [K, N] with N contiguous, but the MFMA wants 8 consecutive K
-//     per lane.  Each thread loads an 8(k) x 8(n) block with eight 16-byte
-//     loads (8 lanes cover 128 contiguous bytes of one row), transposes it in
-//     registers with 32 v_perm_b32, and writes eight 16-byte K-contiguous
-//     column segments: LDS holds B^T [BN x 64].
-//   * LDS rows hold 128 bytes at a 144-byte pitch, so 16 consecutive rows read
-//     at one chunk hit 16 distinct bank groups (no conflicts for the fragment
-//     reads or the stores) and every LDS address is a base plus an immediate.
-//   * Two LDS stages (2 x (BM + BN) x 144 B, 144 KiB at 256 x 256): the global
-//     loads of stage k+1 are in flight while stage k feeds the MFMAs; one
-//     barrier per stage.
-//   * Waves form a 2 x 2 grid; each owns a (BM/2) x (BN/2) sub-tile made of
-//     32 x 32 blocks computed with v_mfma_f32_32x32x16_{bf16,f16}.  The MFMA
-//     computes C^T = B^T A^T (B^T fragment as the first operand) so each lane
-//     ends up with 4 consecutive N values of one row per accumulator group,
-//     stored as one 8-byte write.
+// Data path (run_tile): K advances in stages; A [BM x SBK] and B [SBK x BN]
+// move HBM -> LDS by buffer DMA (16 bytes per lane, no VGPR staging), several
+// stages ahead of the one being multiplied.  A fragments are 128-bit LDS reads;
+// B stays N-contiguous in LDS and is read with the gfx950 transposing read
+// ds_read_b64_tr_b16, so no transpose is ever done in registers.  The MFMA is
+// v_mfma_f32_32x32x16_{bf16,f16}; it computes C^T = B^T A^T so each lane ends
+// up with 4 consecutive N values of a row, stored as one 8-byte write.
 #include "mgg.h"
 #include "mgg_internal.h"
 
@@ -52,10 +40,6 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-constexpr int kThreads = 256;
-constexpr int kBK = 64;                 // K elements per LDS stage
-constexpr int kLdsRow = kBK * 2 + 16;   // LDS row pitch: 8 chunks of 16 bytes + 16 pad
-
 struct Bf16 {
   static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
@@ -78,33 +62,15 @@ struct F16 {
   }
 };
 
-// Byte offset of 16-byte chunk `chunk` (0..7) of LDS row `row`.  The 144-byte
-// pitch (9 x 16 bytes, 9 odd) maps 16 consecutive rows at one chunk onto 16
-// distinct 16-byte bank groups, and keeps every address base + immediate.
-__device__ __forceinline__ int lds_off(int row, int chunk) { return row * kLdsRow + chunk * 16; }
-
 __device__ __forceinline__ u32x4 lds_load(const uint8_t* base, int off) {
   return *reinterpret_cast<const u32x4*>(base + off);
 }
 __device__ __forceinline__ __attribute__((address_space(3))) uint8_t* lds_ptr(uint8_t* p) {
   return (__attribute__((address_space(3))) uint8_t*)p;
 }
-__device__ __forceinline__ void lds_store(uint8_t* base, int off, u32x4 v) {
-  *reinterpret_cast<u32x4*>(base + off) = v;
-}
-// Raw (unswizzled, stride 0) buffer descriptor over `bytes` bytes at `base`;
-// word 3 is the gfx9-family default format.  Larger ranges are clamped to the
-// 32-bit record count: in-tile offsets are far below it.
-constexpr uint32_t kOutOfRange = 0x80000000u;  // any offset >= the record count
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  const int64_t cap = 0x7FFFFFF0LL;
-  const int32_t n = (int32_t)(bytes < 0 ? 0 : (bytes > cap ? cap : bytes));
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
-}
-__device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, int soff) {
-  return __builtin_bit_cast(u32x4,
-                            __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)voff, soff, 0));
-}
+// A voffset at or past every descriptor's record count (records are clamped
+// below 2^31): a DMA lane given it writes zeros to LDS and reads no memory.
+constexpr uint32_t kOutOfRange = 0x80000000u;
 
 // Per-expert tile prefix of the derived queue, built in LDS by the whole
 // workgroup: prefix[e] = sum_{j<e} ceil(max(off[j+1]-off[j],0)/BM) * n_tiles.

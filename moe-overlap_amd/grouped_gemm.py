@@ -63,6 +63,16 @@ def _stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_CU_COUNTS: dict = {}
+
+
+def _cu_count(dev_index: int) -> int:
+    n = _CU_COUNTS.get(dev_index)
+    if n is None:
+        n = _CU_COUNTS[dev_index] = _nat.device_cu_count(dev_index)
+    return n
+
+
 # --------------------------------------------------------------------------
 # expert offsets
 # --------------------------------------------------------------------------
@@ -246,8 +256,9 @@ def persistent_grouped_gemm(
     if block_m not in _SUPPORTED_BLOCKS or block_n not in _SUPPORTED_BLOCKS:
         raise ValueError("block_m and block_n must each be one of 64, 128, 256.")
     device = a_cat.device
+    dev_index = device.index if device.index is not None else torch.cuda.current_device()
     if num_sms is None:
-        num_sms = _nat.device_cu_count(device.index if device.index is not None else torch.cuda.current_device())
+        num_sms = _cu_count(dev_index)
     if int(num_sms) <= 0:
         raise ValueError("num_sms must be positive.")
 
@@ -285,18 +296,21 @@ def persistent_grouped_gemm(
     off32 = expert_offsets if expert_offsets.dtype == torch.int32 else expert_offsets.to(torch.int32)
     off32 = off32.contiguous()
 
+    args = (
+        _DTYPE_CODES[a_cat.dtype], _ptr(a_op), _ptr(b_op), _ptr(c_op),
+        _ptr(off32), m_total, k_pad, n_pad,
+        num_experts, lda, ldb_e, ldb_k, c_op.stride(0),
+        _ptr(we), _ptr(wm), _ptr(wn), num_work,
+        int(block_m), int(block_n), int(num_sms), 1 if use_atomic_queue else 0,
+        _ptr(counter_dev), torch.cuda.current_stream(device).cuda_stream,
+    )
     lib = _nat.lib()
-    with torch.cuda.device(device):
-        _nat.check(
-            lib.mgg_grouped_gemm(
-                _DTYPE_CODES[a_cat.dtype], _ptr(a_op), _ptr(b_op), _ptr(c_op),
-                _ptr(off32), m_total, k_pad, n_pad,
-                num_experts, lda, ldb_e, ldb_k, c_op.stride(0),
-                _ptr(we), _ptr(wm), _ptr(wn), num_work,
-                int(block_m), int(block_n), int(num_sms), 1 if use_atomic_queue else 0,
-                _ptr(counter_dev), _stream_handle(device),
-            )
-        )
+    # The library launches on the calling thread's current HIP device.
+    if torch.cuda.current_device() == dev_index:
+        _nat.check(lib.mgg_grouped_gemm(*args))
+    else:
+        with torch.cuda.device(dev_index):
+            _nat.check(lib.mgg_grouped_gemm(*args))
     if n_pad != n_size:
         return c_op[:, :n_size].contiguous()
     return c_op
