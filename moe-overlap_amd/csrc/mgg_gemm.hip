@@ -72,6 +72,11 @@ __device__ __forceinline__ __attribute__((address_space(3))) uint8_t* lds_ptr(ui
 // below 2^31): a DMA lane given it writes zeros to LDS and reads no memory.
 constexpr uint32_t kOutOfRange = 0x80000000u;
 
+template <int V>
+struct IntConst {
+  static constexpr int value = V;
+};
+
 // Per-expert tile prefix of the derived queue, built in LDS by the whole
 // workgroup: prefix[e] = sum_{j<e} ceil(max(off[j+1]-off[j],0)/BM) * n_tiles.
 // Returns the queue length W = prefix[E].  Same counts as
@@ -149,6 +154,21 @@ __device__ __forceinline__ void wait_dma() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Waits until at most min(later, MAXL) * D of this wave's DMAs are outstanding,
+// i.e. every DMA issued before the last `later` groups of D has completed.
+template <int D, int MAXL>
+__device__ __forceinline__ void wait_dma_groups(int later) {
+  if constexpr (MAXL > 0) {
+    if (later >= MAXL) {
+      wait_dma<MAXL * D>();
+      return;
+    }
+    wait_dma_groups<D, MAXL - 1>(later);
+  } else {
+    wait_dma<0>();
+  }
+}
+
 __device__ __forceinline__ i32x4 make_rsrc4(const void* base, int64_t bytes) {
   const int64_t cap = 0x7FFFFFF0LL;
   const uint64_t addr = reinterpret_cast<uint64_t>(base);
@@ -167,13 +187,14 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // Computes one output tile.  All arguments are uniform across the workgroup,
 // so the early returns never split a barrier.
 //
-// K advances in stages of SBK (32 or 64); NSTAGE stages rotate through LDS.
+// K advances in stages of SBK (16, 32 or 64); NSTAGE stages rotate through LDS.
 // A stage holds A [BM x SBK] as BM rows of 2*SBK bytes and B [SBK x BN] in
 // its global layout (K rows of BN contiguous N values); both arrive by DMA,
 // NSTAGE-1 stages ahead of the one being multiplied.  16-byte chunks are
 // XOR-swizzled on the global side so that the fragment reads below are
 // bank-conflict free:
-//   A row r, chunk c  -> physical chunk c ^ ((r >> 2) & 3)    (SBK == 32)
+//   A row r, chunk c  -> physical chunk c ^ ((r >> 3) & 1)    (SBK == 16)
+//                                        c ^ ((r >> 2) & 3)    (SBK == 32)
 //                                        c ^ ((r >> 1) & 7)    (SBK == 64)
 //   B row k, chunk c  -> physical chunk c ^ 4*(k & 3)          (BN >= 128)
 //                                        c ^ 4*((k >> 1) & 1)  (BN == 64)
@@ -198,7 +219,7 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   constexpr int kBPerWave = kBStage / (1024 * NW);     // B DMAs per wave per stage
   constexpr int kWN = NW / 2;                          // waves along N (2 along M)
   static_assert(kAPerWave >= 1 && kBPerWave >= 1, "tile too small for the wave count");
-  static_assert(kSteps == 2 || kSteps == 4, "K per stage must be 32 or 64");
+  static_assert(kSteps == 1 || kSteps == 2 || kSteps == 4, "K per stage must be 16, 32 or 64");
   static_assert(kStages >= 2, "need at least two LDS stages");
   constexpr int kDmaPerStage = kAPerWave + kBPerWave;
   constexpr int kBChunks = BN / 8;          // 16-byte chunks per B row
@@ -264,7 +285,9 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   // Per-lane DMA source offsets (bytes, stage 0) and the K position of the
   // chunk each lane moves.
   // Chunk (row, K position) moved by lane `lane` in the t-th DMA of a stage.
-  auto a_swz = [](int r) { return kAChunks == 4 ? (r >> 2) & 3 : (r >> 1) & 7; };
+  auto a_swz = [](int r) {
+    return kAChunks == 2 ? (r >> 3) & 1 : kAChunks == 4 ? (r >> 2) & 3 : (r >> 1) & 7;
+  };
   auto a_row = [&](int t) { return kARowsPerDma * (wave * kAPerWave + t) + lane / kAChunks; };
   auto a_kpos = [&](int t) { return 8 * ((lane % kAChunks) ^ a_swz(a_row(t))); };
   auto b_krow = [&](int t) { return (wave * kBPerWave + t) * kBRowsPerDma + lane / kBChunks; };
@@ -289,20 +312,23 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   // stage keeps the stage offset in the SGPR offset; the partial last stage
   // puts it in the VGPR offset and redirects chunks at k >= K past the
   // descriptor, which makes the DMA write zeros.
+  // K < 2^30 (the host bounds (K+8)*ldb_k*2 below 2^31), so stage positions
+  // are 32-bit and the full/partial decision stays in scalar registers.
+  const int k_size = (int)K;
   auto issue_part = [&](int s, int d0, int d1) {
-    const int64_t k0 = (int64_t)s * kBK;
+    const int k0 = s * kBK;
     const int buf = s % kStages;
     const uint32_t la = lds_a0 + buf * kAStage + wave * kAPerWave * 1024;
     const uint32_t lb = lds_b0 + buf * kBStage + wave * kBPerWave * 1024;
-    const bool full = k0 + kBK <= K;
+    const bool full = k0 + kBK <= k_size;
 #pragma unroll
     for (int d = d0; d < d1; ++d) {
       if (d < kAPerWave) {
         const int t = d;
         if (full) {
-          dma16(a_rsrc, a_voff[t], (uint32_t)(k0 * 2), la + t * 1024);
+          dma16(a_rsrc, a_voff[t], (uint32_t)k0 * 2u, la + t * 1024);
         } else {
-          const uint32_t v = k0 + a_kpos(t) < K ? a_voff[t] + (uint32_t)(k0 * 2) : kOutOfRange;
+          const uint32_t v = k0 + a_kpos(t) < k_size ? a_voff[t] + (uint32_t)k0 * 2u : kOutOfRange;
           dma16(a_rsrc, v, 0u, la + t * 1024);
         }
       } else {
@@ -311,7 +337,7 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
           dma16(b_rsrc, b_voff[t], (uint32_t)k0 * b_row_bytes, lb + t * 1024);
         } else {
           const uint32_t v =
-              k0 + b_krow(t) < K ? b_voff[t] + (uint32_t)k0 * b_row_bytes : kOutOfRange;
+              k0 + b_krow(t) < k_size ? b_voff[t] + (uint32_t)k0 * b_row_bytes : kOutOfRange;
           dma16(b_rsrc, v, 0u, lb + t * 1024);
         }
       }
@@ -345,12 +371,14 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  u32x4 fa[2][kMB];  // A fragments of two consecutive 16-wide K steps
-  u32x4 fb[2][kNB];  // B fragments
-  auto read_a = [&](int buf, int kk, int j) {
-    fa[kk & 1][j] = lds_load(lds, a_off[kk] + buf * kAStage + 32 * kARowBytes * j - lds_a0);
+  // Fragments are double-buffered by the parity of the K step's global index
+  // (k0/16): buffer f holds the step being multiplied while the other fills.
+  u32x4 fa[2][kMB];
+  u32x4 fb[2][kNB];
+  auto read_a = [&](int f, int buf, int kk, int j) {
+    fa[f][j] = lds_load(lds, a_off[kk] + buf * kAStage + 32 * kARowBytes * j - lds_a0);
   };
-  auto read_b = [&](int buf, int kk, int i) {
+  auto read_b = [&](int f, int buf, int kk, int i) {
     const uint32_t base = b_off[i] + buf * kBStage + 16 * kk * kBRowBytes - lds_a0;
     const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (lds_i16x4*)(lds_ptr(lds) + base));
@@ -358,22 +386,23 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
         (lds_i16x4*)(lds_ptr(lds) + base + 4 * kBRowBytes));
     const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
     const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
-    fb[kk & 1][i] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+    fb[f][i] = u32x4{l2[0], l2[1], h2[0], h2[1]};
   };
-  auto read_kstep = [&](int buf, int kk, int part) {  // half `part` of a K step's fragments
+  // Half `part` of the fragments of K step kk of LDS buffer `buf`, into fragment buffer f.
+  auto read_kstep = [&](int f, int buf, int kk, int part) {
 #pragma unroll
     for (int j = part * kMB / 2; j < (part + 1) * kMB / 2 + (kMB == 1 && part == 0); ++j)
-      read_a(buf, kk, j);
+      read_a(f, buf, kk, j);
 #pragma unroll
     for (int i = part * kNB / 2; i < (part + 1) * kNB / 2 + (kNB == 1 && part == 0); ++i)
-      read_b(buf, kk, i);
+      read_b(f, buf, kk, i);
   };
-  auto mfma_group = [&](int kk, int g) {  // quarter g of a K step's MFMAs
+  auto mfma_group = [&](int f, int g) {  // quarter g of the MFMAs of fragment buffer f
     constexpr int kPer = kMB * kNB;
 #pragma unroll
     for (int q = g * kPer / 4; q < (g + 1) * kPer / 4; ++q) {
       const int i = q / kMB, j = q % kMB;
-      acc[i][j] = T::mfma(fb[kk & 1][i], fa[kk & 1][j], acc[i][j]);
+      acc[i][j] = T::mfma(fb[f][i], fa[f][j], acc[i][j]);
     }
   };
 
@@ -381,11 +410,7 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   // that stages up to `last_issued` have been issued (each stage is
   // kDmaPerStage DMAs, and DMAs complete in issue order).
   auto wait_stage = [&](int s, int last_issued) {
-    const int later = last_issued - s;  // 0 .. kStages-2
-    if (kStages > 3 && later >= 3) wait_dma<3 * kDmaPerStage>();
-    else if (kStages > 2 && later == 2) wait_dma<2 * kDmaPerStage>();
-    else if (later == 1) wait_dma<kDmaPerStage>();
-    else wait_dma<0>();
+    wait_dma_groups<kDmaPerStage, kStages - 2>(last_issued - s);
   };
 
   const int nk = (int)((K + kBK - 1) / kBK);
@@ -398,63 +423,87 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   wait_stage(0, issued);
   __syncthreads();
   if (nk > 0) {
-    read_kstep(0, 0, 0);
-    read_kstep(0, 0, 1);
+    read_kstep(0, 0, 0, 0);
+    read_kstep(0, 0, 0, 1);
   }
 
   // MFMA groups of a stage in program order.  Each K step's 4 groups are
   // followed by: the next K step's fragment reads (half after group 0, half
   // after group 1, so they have two groups of MFMAs to land), and a share of
   // the DMAs of stage kt+kStages-1 (spread over the early groups so a wave
-  // never stalls behind a burst of them).  In the last K step the barrier
-  // that publishes stage kt+1 comes after group 0 (by then every fragment of
-  // this stage has been read), and stage kt+1's first fragments are read
-  // after groups 1 and 2.
-  constexpr int kEarlyGroups = 4 * (kSteps - 1);
+  // never stalls behind a burst of them; a one-step stage issues them all
+  // first).  In the last K step the barrier that publishes stage kt+1 comes
+  // after group 0 (by then every fragment of this stage has been read), and
+  // stage kt+1's first fragments are read after groups 1 and 2.  P0 is the
+  // fragment buffer of the stage's first K step, a compile-time constant.
+  constexpr int kEarlyGroups = kSteps > 1 ? 4 * (kSteps - 1) : 1;
   auto dma_share = [&](int grp, int s) {
     const int d0 = grp * kDmaPerStage / kEarlyGroups;
     const int d1 = (grp + 1) * kDmaPerStage / kEarlyGroups;
     if (d1 > d0) issue_part(s, d0, d1);
   };
-  auto early_steps = [&](int buf, int next_stage, bool issue) {
+  auto early_steps = [&](auto P0, int buf, int next_stage, bool issue) {
+    constexpr int p0 = decltype(P0)::value;
 #pragma unroll
     for (int kk = 0; kk + 1 < kSteps; ++kk) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        mfma_group(kk, g);
-        if (g < 2) read_kstep(buf, kk + 1, g);
+        mfma_group((p0 + kk) & 1, g);
+        if (g < 2) read_kstep((p0 + kk + 1) & 1, buf, kk + 1, g);
         if (issue) dma_share(kk * 4 + g, next_stage);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
-  // Steady state: every stage but the last has a successor to publish.
-  int kt = 0;
-  for (; kt + 1 < nk; ++kt) {
+  // A stage that has a successor to publish.
+  auto stage = [&](auto P0, int kt) {
+    constexpr int p0 = decltype(P0)::value;
+    constexpr int f_last = (p0 + kSteps - 1) & 1;
+    constexpr int f_next = (p0 + kSteps) & 1;
     const int buf = kt % kStages;
     // Stage kt+kStages-1 goes into the buffer stage kt-1 used; every wave
     // finished reading it before the barrier of stage kt-1.
     const bool issue = kt + kStages - 1 < nk;
     if (issue) issued = kt + kStages - 1;
-    early_steps(buf, kt + kStages - 1, issue);
-    mfma_group(kSteps - 1, 0);
+    if constexpr (kSteps == 1) {
+      if (issue) issue_stage(kt + kStages - 1);
+    }
+    early_steps(P0, buf, kt + kStages - 1, issue);
+    mfma_group(f_last, 0);
     __builtin_amdgcn_sched_barrier(0);
     wait_stage(kt + 1, issued);
     __syncthreads();
     const int nbuf = (kt + 1) % kStages;
-    mfma_group(kSteps - 1, 1);
-    read_kstep(nbuf, 0, 0);
+    mfma_group(f_last, 1);
+    read_kstep(f_next, nbuf, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_group(kSteps - 1, 2);
-    read_kstep(nbuf, 0, 1);
+    mfma_group(f_last, 2);
+    read_kstep(f_next, nbuf, 0, 1);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_group(kSteps - 1, 3);
+    mfma_group(f_last, 3);
     __builtin_amdgcn_sched_barrier(0);
-  }
-  if (nk > 0) {  // the last stage
-    early_steps(kt % kStages, 0, false);
+  };
+  auto last_stage = [&](auto P0, int kt) {
+    constexpr int p0 = decltype(P0)::value;
+    early_steps(P0, kt % kStages, 0, false);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) mfma_group(kSteps - 1, g);
+    for (int g = 0; g < 4; ++g) mfma_group((p0 + kSteps - 1) & 1, g);
+  };
+  int kt = 0;
+  if constexpr (kSteps % 2 == 0) {  // every stage starts on fragment buffer 0
+    for (; kt + 1 < nk; ++kt) stage(IntConst<0>{}, kt);
+    if (nk > 0) last_stage(IntConst<0>{}, kt);
+  } else {  // one-step stages alternate buffers: unrolled by two
+    for (; kt + 2 < nk; kt += 2) {
+      stage(IntConst<0>{}, kt);
+      stage(IntConst<1>{}, kt + 1);
+    }
+    if (kt + 1 < nk) {
+      stage(IntConst<0>{}, kt);
+      last_stage(IntConst<1>{}, kt + 1);
+    } else if (nk > 0) {
+      last_stage(IntConst<0>{}, kt);
+    }
   }
 
   // ---- epilogue: acc[i][j] register r holds D[n][m] of the 32x32 block with
