@@ -83,7 +83,7 @@ struct IntConst {
 // src/triton_grouped_gemm.py:253-271.
 template <int BM, int NT>
 __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_prefix,
-                                 int32_t* s_scan) {
+                                 int32_t* s_offs, int32_t* s_scan) {
   const int tid = threadIdx.x;
   const int E = p.num_experts;
   const int per = (E + NT - 1) / NT;
@@ -111,11 +111,15 @@ __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_pr
     const int e = e0 + i;
     if (e < E) {
       s_prefix[e] = base;
+      if (s_offs != nullptr) s_offs[e] = p.offsets[e];
       const int64_t cnt = (int64_t)p.offsets[e + 1] - (int64_t)p.offsets[e];
       base += cnt > 0 ? (int32_t)(((cnt + BM - 1) / BM) * (int64_t)n_tiles) : 0;
     }
   }
-  if (tid == NT - 1) s_prefix[E] = s_scan[NT - 1];
+  if (tid == NT - 1) {
+    s_prefix[E] = s_scan[NT - 1];
+    if (s_offs != nullptr) s_offs[E] = p.offsets[E];
+  }
   __syncthreads();
   return s_prefix[E];
 }
@@ -184,8 +188,9 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-// Computes one output tile.  All arguments are uniform across the workgroup,
-// so the early returns never split a barrier.
+// One workgroup's share of the queue: a persistent loop over tiles.  All
+// arguments, and every branch below that guards a barrier, are uniform across
+// the workgroup.
 //
 // K advances in stages of SBK (16, 32 or 64); NSTAGE stages rotate through LDS.
 // A stage holds A [BM x SBK] as BM rows of 2*SBK bytes and B [SBK x BN] in
@@ -203,9 +208,16 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // lane s addresses B[k0 + s/4][n0 + 4*(s%4) .. +3] and lane j receives
 // B[k0 .. k0+3][n0 + j], so two reads give a lane the 8 consecutive K of its
 // column that the MFMA expects.
+//
+// Consecutive tiles overlap: once a tile's last stage has been read from LDS,
+// the next tile is decoded and its first stage is issued before the finished
+// tile's stores, so the next tile's first DMA latency hides behind the
+// epilogue; in atomic mode the ticket of the next tile is taken early in the
+// current one.  `first` is this worker's first item (a ticket in atomic mode).
 template <int BM, int BN, int SBK, int NSTAGE, int NW, class T>
-__device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int n_tiles,
-                                         const int32_t* s_prefix, uint8_t* lds) {
+__device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32_t first,
+                                           int n_tiles, const int32_t* s_prefix,
+                                           const int32_t* s_offs, int32_t* s_item, uint8_t* lds) {
   constexpr int kBK = SBK;                  // K per stage
   constexpr int kStages = NSTAGE;           // LDS stages in rotation
   constexpr int kSteps = kBK / 16;          // MFMA K steps per stage
@@ -233,88 +245,107 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1;
   const int wn = wave >> 1;
-
-  int e, tm, tn;
-  if (p.num_work >= 0) {
-    e = p.q_expert[item];
-    tm = p.q_tile_m[item];
-    tn = p.q_tile_n[item];
-    if ((uint32_t)e >= (uint32_t)p.num_experts || tm < 0 || (uint32_t)tn >= (uint32_t)n_tiles)
-      return;
-  } else {
-    int lo = 0, hi = p.num_experts - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_prefix[mid] <= item) lo = mid; else hi = mid - 1;
-    }
-    e = lo;
-    const int32_t local = item - s_prefix[e];
-    tm = local / n_tiles;
-    tn = local - tm * n_tiles;
-  }
-  // Uniform across the workgroup (LDS reads look divergent to the compiler):
-  // keep the tile coordinates, and everything derived from them, in SGPRs.
-  e = __builtin_amdgcn_readfirstlane(e);
-  tm = __builtin_amdgcn_readfirstlane(tm);
-  tn = __builtin_amdgcn_readfirstlane(tn);
-
-  const int64_t row0 = p.offsets[e];
-  const int64_t cnt = (int64_t)p.offsets[e + 1] - row0;
-  const int64_t m0 = (int64_t)tm * BM;
-  const int64_t left = cnt - m0;
-  if (left <= 0) return;
-  const int rows_valid = left < BM ? (int)left : BM;
-  const int64_t n0 = (int64_t)tn * BN;
+  const int G = gridDim.x;
   const int64_t K = p.k;
+  // K < 2^30 (the host bounds (K+8)*ldb_k*2 below 2^31), so stage positions
+  // are 32-bit and the full/partial decision stays in scalar registers.
+  const int k_size = (int)K;
+  const int nk = (int)((K + kBK - 1) / kBK);
   const int64_t last_row = p.m - 1;
 
-  // ---- global sources ----------------------------------------------------
+  // ---- tile decode ---------------------------------------------------------
+  // The output tile of queue item `item`: expert e, rows [row_base,
+  // row_base + rows_valid) of C, columns [n0, n0 + BN).  False for an item a
+  // caller-built queue fills with an out-of-range or empty tile (skipped).
+  struct Coords {
+    int32_t e;
+    int64_t row_base;
+    int rows_valid;
+    int64_t n0;
+  };
+  auto decode = [&](int32_t item, Coords& c) -> bool {
+    int e, tm, tn;
+    if (p.num_work >= 0) {
+      e = p.q_expert[item];
+      tm = p.q_tile_m[item];
+      tn = p.q_tile_n[item];
+    } else {
+      int lo = 0, hi = p.num_experts - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_prefix[mid] <= item) lo = mid; else hi = mid - 1;
+      }
+      e = lo;
+      const int32_t local = item - s_prefix[e];
+      tm = local / n_tiles;
+      tn = local - tm * n_tiles;
+    }
+    // Uniform across the workgroup (memory reads look divergent to the
+    // compiler): keep the coordinates, and all derived from them, in SGPRs.
+    e = __builtin_amdgcn_readfirstlane(e);
+    tm = __builtin_amdgcn_readfirstlane(tm);
+    tn = __builtin_amdgcn_readfirstlane(tn);
+    if ((uint32_t)e >= (uint32_t)p.num_experts || tm < 0 || (uint32_t)tn >= (uint32_t)n_tiles)
+      return false;
+    const int32_t off_lo = __builtin_amdgcn_readfirstlane(s_offs != nullptr ? s_offs[e] : p.offsets[e]);
+    const int32_t off_hi =
+        __builtin_amdgcn_readfirstlane(s_offs != nullptr ? s_offs[e + 1] : p.offsets[e + 1]);
+    const int64_t m0 = (int64_t)tm * BM;
+    const int64_t left = (int64_t)off_hi - off_lo - m0;
+    if (left <= 0) return false;
+    c.e = e;
+    c.row_base = off_lo + m0;
+    c.rows_valid = left < BM ? (int)left : BM;
+    c.n0 = (int64_t)tn * BN;
+    return true;
+  };
+
+  // ---- DMA sources ---------------------------------------------------------
   // Each descriptor ends exactly at the last element of its operand, so a
   // DMA past it writes zeros: rows of A past M, rows of B past K.  Rows of A
   // inside [0, M) but past this expert's count bring the next expert's data;
   // their results are never stored.  B columns past N (edge tiles) are
   // clamped onto the last 8 columns.  Offsets are 32-bit (the host bounds
   // lda and ldb_k).
-  int64_t r0 = row0 + m0;
-  r0 = r0 < 0 ? 0 : (r0 > p.m ? p.m : r0);
-  const int64_t a_end = r0 < p.m ? ((p.m - 1 - r0) * p.lda + K) * 2 : 0;
-  const i32x4 a_rsrc = make_rsrc4(p.a + r0 * p.lda, a_end);
-  const int64_t b_end = ((K - 1) * p.ldb_k + p.n - n0) * 2;
-  const i32x4 b_rsrc = make_rsrc4(p.b + (int64_t)e * p.ldb_e + n0, b_end);
-
-  // Per-lane DMA source offsets (bytes, stage 0) and the K position of the
-  // chunk each lane moves.
-  // Chunk (row, K position) moved by lane `lane` in the t-th DMA of a stage.
   auto a_swz = [](int r) {
     return kAChunks == 2 ? (r >> 3) & 1 : kAChunks == 4 ? (r >> 2) & 3 : (r >> 1) & 7;
   };
+  // Chunk (row, K position) moved by lane `lane` in the t-th DMA of a stage.
   auto a_row = [&](int t) { return kARowsPerDma * (wave * kAPerWave + t) + lane / kAChunks; };
   auto a_kpos = [&](int t) { return 8 * ((lane % kAChunks) ^ a_swz(a_row(t))); };
   auto b_krow = [&](int t) { return (wave * kBPerWave + t) * kBRowsPerDma + lane / kBChunks; };
-  uint32_t a_voff[kAPerWave];
+  uint32_t a_voff[kAPerWave];  // per-lane source offsets (bytes, stage 0), the same for every tile
 #pragma unroll
   for (int t = 0; t < kAPerWave; ++t) a_voff[t] = (uint32_t)((a_row(t) * p.lda + a_kpos(t)) * 2);
-  uint32_t b_voff[kBPerWave];
-#pragma unroll
-  for (int t = 0; t < kBPerWave; ++t) {
-    const int k = b_krow(t);
-    const int swz = BN >= 128 ? 4 * (k & 3) : 4 * ((k >> 1) & 1);
-    int64_t col = 8 * ((lane % kBChunks) ^ swz);
-    col = n0 + col > p.n - 8 ? p.n - 8 - n0 : col;
-    b_voff[t] = (uint32_t)((k * p.ldb_k + col) * 2);
-  }
   const uint32_t b_row_bytes = (uint32_t)(p.ldb_k * 2);
   const uint32_t lds_a0 = lds_addr(lds);
   const uint32_t lds_b0 = lds_a0 + kStages * kAStage;
+
+  // The DMA state of the tile whose stages are being issued.
+  i32x4 a_rsrc, b_rsrc;
+  uint32_t b_voff[kBPerWave];
+  auto set_sources = [&](const Coords& c) {
+    int64_t r0 = c.row_base;
+    r0 = r0 < 0 ? 0 : (r0 > p.m ? p.m : r0);
+    const int64_t a_end = r0 < p.m ? ((p.m - 1 - r0) * p.lda + K) * 2 : 0;
+    a_rsrc = make_rsrc4(p.a + r0 * p.lda, a_end);
+    const int64_t b_end = ((K - 1) * p.ldb_k + p.n - c.n0) * 2;
+    b_rsrc = make_rsrc4(p.b + (int64_t)c.e * p.ldb_e + c.n0, b_end);
+#pragma unroll
+    for (int t = 0; t < kBPerWave; ++t) {
+      const int k = b_krow(t);
+      const int swz = BN >= 128 ? 4 * (k & 3) : 4 * ((k >> 1) & 1);
+      int64_t col = 8 * ((lane % kBChunks) ^ swz);
+      col = c.n0 + col > p.n - 8 ? p.n - 8 - c.n0 : col;
+      b_voff[t] = (uint32_t)((k * p.ldb_k + col) * 2);
+    }
+  };
 
   // Issues DMAs [d0, d1) of this wave's kDmaPerStage DMAs of stage s (the
   // first kAPerWave move A, the rest B) into LDS buffer s % kStages.  A full
   // stage keeps the stage offset in the SGPR offset; the partial last stage
   // puts it in the VGPR offset and redirects chunks at k >= K past the
   // descriptor, which makes the DMA write zeros.
-  // K < 2^30 (the host bounds (K+8)*ldb_k*2 below 2^31), so stage positions
-  // are 32-bit and the full/partial decision stays in scalar registers.
-  const int k_size = (int)K;
   auto issue_part = [&](int s, int d0, int d1) {
     const int k0 = s * kBK;
     const int buf = s % kStages;
@@ -364,13 +395,6 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   }
 
   f32x16 acc[kNB][kMB];
-#pragma unroll
-  for (int i = 0; i < kNB; ++i)
-#pragma unroll
-    for (int j = 0; j < kMB; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
   // Fragments are double-buffered by the parity of the K step's global index
   // (k0/16): buffer f holds the step being multiplied while the other fills.
   u32x4 fa[2][kMB];
@@ -413,20 +437,6 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
     wait_dma_groups<kDmaPerStage, kStages - 2>(last_issued - s);
   };
 
-  const int nk = (int)((K + kBK - 1) / kBK);
-  __syncthreads();  // the previous tile's waves are done reading the LDS stages
-  // Prologue: stages 0 .. kStages-2 in flight, wait for stage 0.
-  int issued = -1;
-#pragma unroll
-  for (int s = 0; s < kStages - 1; ++s)
-    if (s < nk) issue_stage(issued = s);
-  wait_stage(0, issued);
-  __syncthreads();
-  if (nk > 0) {
-    read_kstep(0, 0, 0, 0);
-    read_kstep(0, 0, 0, 1);
-  }
-
   // MFMA groups of a stage in program order.  Each K step's 4 groups are
   // followed by: the next K step's fragment reads (half after group 0, half
   // after group 1, so they have two groups of MFMAs to land), and a share of
@@ -436,6 +446,7 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
   // after group 0 (by then every fragment of this stage has been read), and
   // stage kt+1's first fragments are read after groups 1 and 2.  P0 is the
   // fragment buffer of the stage's first K step, a compile-time constant.
+  int issued = -1;
   constexpr int kEarlyGroups = kSteps > 1 ? 4 * (kSteps - 1) : 1;
   auto dma_share = [&](int grp, int s) {
     const int d0 = grp * kDmaPerStage / kEarlyGroups;
@@ -489,51 +500,130 @@ __device__ __forceinline__ void run_tile(const GemmParams& p, int32_t item, int 
 #pragma unroll
     for (int g = 0; g < 4; ++g) mfma_group((p0 + kSteps - 1) & 1, g);
   };
-  int kt = 0;
-  if constexpr (kSteps % 2 == 0) {  // every stage starts on fragment buffer 0
-    for (; kt + 1 < nk; ++kt) stage(IntConst<0>{}, kt);
-    if (nk > 0) last_stage(IntConst<0>{}, kt);
-  } else {  // one-step stages alternate buffers: unrolled by two
-    for (; kt + 2 < nk; kt += 2) {
-      stage(IntConst<0>{}, kt);
-      stage(IntConst<1>{}, kt + 1);
+  // All stages of the current tile; stages 0 .. min(kStages-1, nk)-1 have
+  // been issued.  Returns after the last stage's fragments have been read
+  // and its MFMAs issued.
+  auto main_loop = [&](bool take_ticket, int32_t& ticket) {
+#pragma unroll
+    for (int i = 0; i < kNB; ++i)
+#pragma unroll
+      for (int j = 0; j < kMB; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    wait_stage(0, issued);
+    __syncthreads();
+    // The next tile's ticket, taken after the first wait so that this
+    // wave's first DMA wait does not also wait for the atomic.
+    if (take_ticket && tid == 0) ticket = atomicAdd(p.counter, 1);
+    if (nk > 0) {
+      read_kstep(0, 0, 0, 0);
+      read_kstep(0, 0, 0, 1);
     }
-    if (kt + 1 < nk) {
-      stage(IntConst<0>{}, kt);
-      last_stage(IntConst<1>{}, kt + 1);
-    } else if (nk > 0) {
-      last_stage(IntConst<0>{}, kt);
+    int kt = 0;
+    if constexpr (kSteps % 2 == 0) {  // every stage starts on fragment buffer 0
+      for (; kt + 1 < nk; ++kt) stage(IntConst<0>{}, kt);
+      if (nk > 0) last_stage(IntConst<0>{}, kt);
+    } else {  // one-step stages alternate buffers: unrolled by two
+      for (; kt + 2 < nk; kt += 2) {
+        stage(IntConst<0>{}, kt);
+        stage(IntConst<1>{}, kt + 1);
+      }
+      if (kt + 1 < nk) {
+        stage(IntConst<0>{}, kt);
+        last_stage(IntConst<1>{}, kt + 1);
+      } else if (nk > 0) {
+        last_stage(IntConst<0>{}, kt);
+      }
     }
-  }
+  };
 
   // ---- epilogue: acc[i][j] register r holds D[n][m] of the 32x32 block with
   // n = 8*(r/4) + 4*(lane/32) + r%4, m = lane%32 (D = C^T).
-  const int64_t c_row_base = row0 + m0;
+  auto epilogue = [&](const Coords& c) {
 #pragma unroll
-  for (int j = 0; j < kMB; ++j) {
-    const int m = wm * (BM / 2) + 32 * j + frag_row;
-    const int64_t grow = c_row_base + m;
-    const bool row_ok = m < rows_valid && grow >= 0 && grow <= last_row;
-    uint16_t* crow = p.c + grow * p.ldc;
+    for (int j = 0; j < kMB; ++j) {
+      const int m = wm * (BM / 2) + 32 * j + frag_row;
+      const int64_t grow = c.row_base + m;
+      const bool row_ok = m < c.rows_valid && grow >= 0 && grow <= last_row;
+      uint16_t* crow = p.c + grow * p.ldc;
 #pragma unroll
-    for (int i = 0; i < kNB; ++i) {
+      for (int i = 0; i < kNB; ++i) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int64_t n = n0 + wn * (BN / kWN) + 32 * i + 8 * g + 4 * half;
-        if (row_ok && n < p.n) {
-          u32x2 v;
-          v[0] = T::pack(acc[i][j][4 * g + 0], acc[i][j][4 * g + 1]);
-          v[1] = T::pack(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
-          *reinterpret_cast<u32x2*>(crow + n) = v;
+        for (int g = 0; g < 4; ++g) {
+          const int64_t n = c.n0 + wn * (BN / kWN) + 32 * i + 8 * g + 4 * half;
+          if (row_ok && n < p.n) {
+            u32x2 v;
+            v[0] = T::pack(acc[i][j][4 * g + 0], acc[i][j][4 * g + 1]);
+            v[1] = T::pack(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+            *reinterpret_cast<u32x2*>(crow + n) = v;
+          }
         }
       }
     }
+  };
+
+  // ---- the persistent loop -------------------------------------------------
+  // Blocking ticket (used for the first item and to skip a caller queue's
+  // invalid items): the leader takes it and broadcasts it through LDS.
+  auto take_ticket_now = [&]() -> int32_t {
+    if (tid == 0) *s_item = atomicAdd(p.counter, 1);
+    __syncthreads();
+    const int32_t t = *s_item;
+    __syncthreads();
+    return t;
+  };
+  auto advance = [&](int32_t item) -> int32_t { return p.atomic ? take_ticket_now() : item + G; };
+  // The first valid item at or after `item` (W or more when none is left).
+  auto find_valid = [&](int32_t item, Coords& c) -> int32_t {
+    while ((uint32_t)item < (uint32_t)W && !decode(item, c)) item = advance(item);
+    return item;
+  };
+
+  Coords cur;
+  int32_t w = find_valid(first, cur);
+  if ((uint32_t)w >= (uint32_t)W) return;
+  set_sources(cur);
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s)
+    if (s < nk) issue_stage(issued = s);
+  for (;;) {
+    int32_t ticket = 0;
+    main_loop(p.atomic != 0, ticket);
+    // The next item: the ticket taken during this tile, or the next stripe.
+    if (p.atomic && tid == 0) *s_item = ticket;
+    __syncthreads();  // every wave is done reading this tile's LDS stages; s_item is visible
+    int32_t next = p.atomic ? *s_item : w + G;
+    Coords nxt;
+    next = find_valid(next, nxt);
+    const bool more = (uint32_t)next < (uint32_t)W;
+    // The next tile's first stage goes out before this tile's stores and its
+    // other prologue stages after them, so each later wait only ever counts
+    // DMAs issued after the stage it waits for.
+    issued = -1;
+    if (more) {
+      set_sources(nxt);
+      if (nk > 0) issue_stage(issued = 0);
+    }
+    epilogue(cur);
+    if (!more) break;
+#pragma unroll
+    for (int s = 1; s < kStages - 1; ++s)
+      if (s < nk) issue_stage(issued = s);
+    cur = nxt;
+    w = next;
   }
 }
 
 template <int BM, int BN, int SBK, int NSTAGE>
 constexpr int lds_bytes() {
   return NSTAGE * (BM + BN) * SBK * 2;
+}
+// Row offsets of the derived queue's experts are kept in LDS when they fit
+// beside the stages (otherwise each tile reads them from global memory).
+template <int BM, int BN, int SBK, int NSTAGE, int NT>
+constexpr bool offsets_in_lds() {
+  return lds_bytes<BM, BN, SBK, NSTAGE>() + 2 * 4 * (kMaxLdsExpertsGemm + 1) + 4 * NT + 256 <=
+         160 * 1024;
 }
 
 // NW waves per workgroup (4: one per SIMD; 8: two per SIMD, so one wave's
@@ -545,8 +635,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64),
 grouped_gemm_kernel(GemmParams p) {
   static_assert(lds_bytes<BM, BN, SBK, NSTAGE>() <= 144 * 1024, "LDS stages exceed the budget");
   constexpr int NT = NW * 64;
+  constexpr bool kOffsLds = offsets_in_lds<BM, BN, SBK, NSTAGE, NT>();
   __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes<BM, BN, SBK, NSTAGE>()];
   __shared__ int32_t s_prefix[kMaxLdsExpertsGemm + 1];
+  __shared__ int32_t s_offs[kOffsLds ? kMaxLdsExpertsGemm + 1 : 1];
   __shared__ int32_t s_scan[NT];
   __shared__ int32_t s_item;
 
@@ -554,8 +646,10 @@ grouped_gemm_kernel(GemmParams p) {
   const int G = gridDim.x;
   const int n_tiles = (int)((p.n + BN - 1) / BN);
 
-  const int32_t W =
-      p.num_work >= 0 ? p.num_work : derive_prefix<BM, NT>(p, n_tiles, s_prefix, s_scan);
+  const int32_t W = p.num_work >= 0
+                        ? p.num_work
+                        : derive_prefix<BM, NT>(p, n_tiles, s_prefix, kOffsLds ? s_offs : nullptr,
+                                                s_scan);
   if (W == 0) {
     zero_fill(p);
     return;
@@ -567,20 +661,18 @@ grouped_gemm_kernel(GemmParams p) {
   int v = blockIdx.x;
   if (p.remap_xcd && (G & 7) == 0) v = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
 
-  // Striped: items v, v+G, v+2G, ...  Atomic: the leader thread takes the
-  // next ticket from the global counter and broadcasts it through LDS.
-  auto next_ticket = [&]() -> int32_t {
+  // Striped: items v, v+G, v+2G, ...  Atomic: tickets from the global
+  // counter, the first one taken here (the leader broadcasts it via LDS).
+  int32_t first = v;
+  if (p.atomic) {
     if (tid == 0) s_item = atomicAdd(p.counter, 1);
     __syncthreads();
-    const int32_t t = s_item;
+    first = s_item;
     __syncthreads();
-    return t;
-  };
-  int32_t w = p.atomic ? next_ticket() : v;
-  while ((uint32_t)w < (uint32_t)W) {
-    run_tile<BM, BN, SBK, NSTAGE, NW, T>(p, w, n_tiles, s_prefix, lds);
-    w = p.atomic ? next_ticket() : w + G;
   }
+  run_worker<BM, BN, SBK, NSTAGE, NW, T>(p, W, first, n_tiles, s_prefix,
+                                         (kOffsLds && p.num_work < 0) ? s_offs : nullptr,
+                                         &s_item, lds);
   if (!p.atomic) return;
   // Every worker has fetched its final (out-of-range) ticket before adding to
   // `done`, so the last one to arrive reads the final count (W + G when no
