@@ -21,6 +21,18 @@
  *                                     tile kernels of :36-233
  *   mgg_device_cu_count            -> the `num_sms` grid size the reference
  *                                     passes by hand (:330, :375)
+ *   mgg_grouped_gemm_ex            -> the expert MLP's two GEMMs with the
+ *                                     activation fused in
+ *                                     (src/train_moe_baseline.py:239-242)
+ *   mgg_dispatch_layout            -> sort / bincount / cumsum / inv_perm of
+ *                                     src/train_moe_baseline.py:219-237 (and the
+ *                                     per-expert counts of DeepEP's
+ *                                     csrc/kernels/layout.cu:10-121)
+ *   mgg_gather_rows                -> grouped_tokens = valid_tokens[perm]
+ *                                     (src/train_moe_baseline.py:224)
+ *   mgg_combine_rows               -> out[valid] = grouped_out[inv_perm] and
+ *                                     out += y * gate over the top-k slots
+ *                                     (src/train_moe_baseline.py:245-246, :340-341)
  */
 #ifndef MGG_H_
 #define MGG_H_
@@ -40,6 +52,11 @@ extern "C" {
 /* Element types of the GEMM operands. */
 #define MGG_DTYPE_BF16 0
 #define MGG_DTYPE_FP16 1
+
+/* Fused GEMM epilogues (mgg_grouped_gemm_ex). */
+#define MGG_EPI_NONE 0
+#define MGG_EPI_GELU 1   /* C = gelu(A @ B), erf form (torch.nn.functional.gelu) */
+#define MGG_EPI_SWIGLU 2 /* C = silu(A @ Bgate) * (A @ Bup), B columns interleaved */
 
 /* Integer types of the per-expert count vector. */
 #define MGG_INT32 0
@@ -127,6 +144,64 @@ int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
                      const int32_t* work_expert, const int32_t* work_tile_m,
                      const int32_t* work_tile_n, int64_t num_work, int block_m, int block_n,
                      int num_workers, int use_atomic_queue, int32_t* work_counter, void* stream);
+
+/*
+ * mgg_grouped_gemm with a fused element-wise epilogue and the queue always
+ * derived on the device.  Same arguments and semantics otherwise.
+ *   MGG_EPI_GELU:   C[r, n] = gelu(sum_k A[r, k] B[e, k, n]) (fp32, then rounded).
+ *   MGG_EPI_SWIGLU: B's N columns hold gate and up projections interleaved in
+ *                   groups of 64: columns 64q .. 64q+31 are gate outputs
+ *                   32q .. 32q+31, columns 64q+32 .. 64q+63 the up outputs of
+ *                   the same indices.  C has N/2 columns:
+ *                   C[r, f] = silu(gate[r, f]) * up[r, f].  N % 64 == 0.
+ * Fused epilogues are compiled for block_m == block_n in {128, 256}.
+ * (Introduced with ABI version 2.)
+ */
+int mgg_grouped_gemm_ex(int dtype, int epilogue, const void* a, const void* b, void* c,
+                        const int32_t* expert_offsets, int64_t m_size, int64_t k_size,
+                        int64_t n_size, int64_t num_experts, int64_t lda, int64_t ldb_e,
+                        int64_t ldb_k, int64_t ldc, int block_m, int block_n, int num_workers,
+                        int use_atomic_queue, int32_t* work_counter, void* stream);
+
+/*
+ * Dispatch layout of T tokens routed to top_k experts each (one GPU's share):
+ *   topk_idx  [T, top_k] int32 or int64 (idx_type), row-major, on the device;
+ *             entries outside [0, E) (e.g. -1) are masked assignments.
+ * Outputs (device, int32):
+ *   counts[E]            assignments per expert;
+ *   offsets[E+1]         exclusive prefix of counts (offsets[E] = valid total);
+ *   slot_position[T*k]   row of assignment a = t*top_k + j in the expert-major
+ *                        order (stable: by a within an expert), -1 if masked;
+ *   token_index[T*k]     for rows p < offsets[E]: the token of row p;
+ *   row_assignment[T*k]  for rows p < offsets[E]: the assignment a of row p.
+ * workspace: device memory of mgg_dispatch_layout_workspace_bytes() bytes
+ * (overwritten).  E <= 8192, T*top_k < 2^31.  No host synchronisation.
+ */
+int64_t mgg_dispatch_layout_workspace_bytes(int64_t num_tokens, int top_k, int64_t num_experts);
+int mgg_dispatch_layout(const void* topk_idx, int idx_type, int64_t num_tokens, int top_k,
+                        int64_t num_experts, int32_t* counts, int32_t* offsets,
+                        int32_t* slot_position, int32_t* token_index, int32_t* row_assignment,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * out[p, :] = x[token_index[p], :] for p < rows, rows = *num_rows (device
+ * int32, e.g. offsets + E from mgg_dispatch_layout) clamped to max_rows, or
+ * max_rows when num_rows is null.  Rows of `hidden` BF16/FP16 elements with
+ * leading dimensions ld_x, ld_out.
+ */
+int mgg_gather_rows(int dtype, const void* x, int64_t ld_x, const int32_t* token_index,
+                    const int32_t* num_rows, int64_t max_rows, int64_t hidden, void* out,
+                    int64_t ld_out, void* stream);
+
+/*
+ * out[t, :] = sum_{j < top_k, slot_position[t*top_k+j] >= 0}
+ *             weights[t*top_k+j] * y[slot_position[t*top_k+j], :]
+ * for t < num_tokens: fp32 accumulation in slot order, one rounding to the
+ * output type (BF16/FP16, same as y).  weights: fp32 [T, top_k] on the device.
+ */
+int mgg_combine_rows(int dtype, const void* y, int64_t ld_y, const int32_t* slot_position,
+                     const float* weights, int64_t num_tokens, int top_k, int64_t hidden,
+                     void* out, int64_t ld_out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -44,8 +44,6 @@ int counters_for(hipStream_t stream, int32_t** out) {
   return MGG_OK;
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
 }  // namespace
 
 int set_error(int code, const std::string& msg) {
@@ -66,7 +64,7 @@ using mgg::set_error;
 
 extern "C" {
 
-int mgg_abi_version(void) { return 1; }
+int mgg_abi_version(void) { return 2; }
 
 const char* mgg_last_error(void) { return mgg::g_last_error.c_str(); }
 
@@ -166,26 +164,38 @@ int mgg_build_work_queue_host(const int64_t* expert_offsets, int64_t num_experts
   return MGG_OK;
 }
 
-int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
-                     const int32_t* expert_offsets, int64_t m_size, int64_t k_size, int64_t n_size,
-                     int64_t num_experts, int64_t lda, int64_t ldb_e, int64_t ldb_k, int64_t ldc,
-                     const int32_t* work_expert, const int32_t* work_tile_m,
-                     const int32_t* work_tile_n, int64_t num_work, int block_m, int block_n,
-                     int num_workers, int use_atomic_queue, int32_t* work_counter, void* stream) {
-  mgg::clear_error();
-  const hipStream_t st = static_cast<hipStream_t>(stream);
+}  // extern "C"
+
+namespace mgg {
+namespace {
+
+// Validation and launch shared by mgg_grouped_gemm and mgg_grouped_gemm_ex.
+int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, void* c,
+                      const int32_t* expert_offsets, int64_t m_size, int64_t k_size,
+                      int64_t n_size, int64_t num_experts, int64_t lda, int64_t ldb_e,
+                      int64_t ldb_k, int64_t ldc, const int32_t* work_expert,
+                      const int32_t* work_tile_m, const int32_t* work_tile_n, int64_t num_work,
+                      int block_m, int block_n, int num_workers, int use_atomic_queue,
+                      int32_t* work_counter, hipStream_t st) {
   if (dtype != MGG_DTYPE_BF16 && dtype != MGG_DTYPE_FP16)
     return set_error(MGG_ERR_UNSUPPORTED, "dtype must be MGG_DTYPE_BF16 or MGG_DTYPE_FP16");
+  if (epilogue != MGG_EPI_NONE && epilogue != MGG_EPI_GELU && epilogue != MGG_EPI_SWIGLU)
+    return set_error(MGG_ERR_INVALID, "epilogue must be MGG_EPI_NONE, MGG_EPI_GELU or MGG_EPI_SWIGLU");
   const bool block_ok = (block_m == 64 || block_m == 128 || block_m == 256) &&
                         (block_n == 64 || block_n == 128 || block_n == 256);
   if (!block_ok)
     return set_error(MGG_ERR_UNSUPPORTED, "block_m/block_n must each be one of 64, 128, 256");
+  if (!epilogue_supported(epilogue, block_m, block_n))
+    return set_error(MGG_ERR_UNSUPPORTED, "fused epilogues need block_m == block_n in {128, 256}");
   if (m_size < 0 || k_size < 0 || n_size < 0 || num_experts < 0)
     return set_error(MGG_ERR_INVALID, "sizes must be >= 0");
   if (m_size == 0 || n_size == 0) return MGG_OK;  // C has no elements
   if (k_size % 8 != 0 || n_size % 8 != 0)
     return set_error(MGG_ERR_UNSUPPORTED, "K and N must be multiples of 8");
-  if (lda < k_size || ldb_k < n_size || ldc < n_size || ldb_e < 0)
+  if (epilogue == MGG_EPI_SWIGLU && n_size % 64 != 0)
+    return set_error(MGG_ERR_UNSUPPORTED, "SwiGLU needs N (gate and up columns) a multiple of 64");
+  const int64_t c_cols = epilogue == MGG_EPI_SWIGLU ? n_size / 2 : n_size;
+  if (lda < k_size || ldb_k < n_size || ldc < c_cols || ldb_e < 0)
     return set_error(MGG_ERR_INVALID, "leading dimensions smaller than the matrix extents");
   if (lda % 8 != 0 || ldb_k % 8 != 0 || ldb_e % 8 != 0 || ldc % 8 != 0)
     return set_error(MGG_ERR_UNSUPPORTED, "strides must be multiples of 8 elements");
@@ -193,7 +203,7 @@ int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
   const bool reads_ab = num_experts > 0 && k_size > 0;
   if (c == nullptr || expert_offsets == nullptr || (reads_ab && (a == nullptr || b == nullptr)))
     return set_error(MGG_ERR_INVALID, "null operand pointer");
-  if (!mgg::aligned16(a) || !mgg::aligned16(b) || !mgg::aligned16(c))
+  if (!aligned16(a) || !aligned16(b) || !aligned16(c))
     return set_error(MGG_ERR_UNSUPPORTED, "operand base pointers must be 16-byte aligned");
   // In-tile byte offsets are 32-bit: BM rows of A, K+8 rows of B.
   const int64_t lim = ((int64_t)1 << 31) - 4096;
@@ -204,9 +214,9 @@ int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
   if (workers <= 0) {
     int device = 0;
     hipError_t err = hipGetDevice(&device);
-    if (err != hipSuccess) return mgg::hip_error(err, "hipGetDevice");
+    if (err != hipSuccess) return hip_error(err, "hipGetDevice");
     err = hipDeviceGetAttribute(&workers, hipDeviceAttributeMultiprocessorCount, device);
-    if (err != hipSuccess) return mgg::hip_error(err, "hipDeviceGetAttribute");
+    if (err != hipSuccess) return hip_error(err, "hipDeviceGetAttribute");
   }
   if (workers > 65536) return set_error(MGG_ERR_INVALID, "num_workers must be <= 65536");
 
@@ -217,7 +227,7 @@ int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
     if (num_work + workers >= ((int64_t)1 << 31))
       return set_error(MGG_ERR_INVALID, "num_work + num_workers must be < 2^31");
   } else {
-    if (num_experts > mgg::kMaxLdsExpertsGemm)
+    if (num_experts > kMaxLdsExpertsGemm)
       return set_error(MGG_ERR_UNSUPPORTED,
                        "the device-derived queue supports at most 2048 experts; pass a "
                        "prebuilt queue");
@@ -227,7 +237,7 @@ int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
       return set_error(MGG_ERR_INVALID, "queue length may exceed 2^31");
   }
 
-  mgg::GemmParams p{};
+  GemmParams p{};
   p.a = static_cast<const uint16_t*>(a);
   p.b = static_cast<const uint16_t*>(b);
   p.c = static_cast<uint16_t*>(c);
@@ -248,13 +258,107 @@ int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
   p.remap_xcd = 1;
   if (p.atomic) {
     int32_t* counters = nullptr;
-    const int rc = mgg::counters_for(st, &counters);
+    const int rc = counters_for(st, &counters);
     if (rc != MGG_OK) return rc;
     p.counter = counters;
     p.done = counters + 1;
     p.report = work_counter;
   }
-  return mgg::launch_grouped_gemm(dtype, block_m, block_n, p, workers, st);
+  return launch_grouped_gemm(dtype, epilogue, block_m, block_n, p, workers, st);
+}
+
+}  // namespace
+}  // namespace mgg
+
+extern "C" {
+
+int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
+                     const int32_t* expert_offsets, int64_t m_size, int64_t k_size, int64_t n_size,
+                     int64_t num_experts, int64_t lda, int64_t ldb_e, int64_t ldb_k, int64_t ldc,
+                     const int32_t* work_expert, const int32_t* work_tile_m,
+                     const int32_t* work_tile_n, int64_t num_work, int block_m, int block_n,
+                     int num_workers, int use_atomic_queue, int32_t* work_counter, void* stream) {
+  mgg::clear_error();
+  return mgg::grouped_gemm_impl(dtype, MGG_EPI_NONE, a, b, c, expert_offsets, m_size, k_size,
+                                n_size, num_experts, lda, ldb_e, ldb_k, ldc, work_expert,
+                                work_tile_m, work_tile_n, num_work, block_m, block_n, num_workers,
+                                use_atomic_queue, work_counter, static_cast<hipStream_t>(stream));
+}
+
+int mgg_grouped_gemm_ex(int dtype, int epilogue, const void* a, const void* b, void* c,
+                        const int32_t* expert_offsets, int64_t m_size, int64_t k_size,
+                        int64_t n_size, int64_t num_experts, int64_t lda, int64_t ldb_e,
+                        int64_t ldb_k, int64_t ldc, int block_m, int block_n, int num_workers,
+                        int use_atomic_queue, int32_t* work_counter, void* stream) {
+  mgg::clear_error();
+  return mgg::grouped_gemm_impl(dtype, epilogue, a, b, c, expert_offsets, m_size, k_size, n_size,
+                                num_experts, lda, ldb_e, ldb_k, ldc, nullptr, nullptr, nullptr, -1,
+                                block_m, block_n, num_workers, use_atomic_queue, work_counter,
+                                static_cast<hipStream_t>(stream));
+}
+
+int64_t mgg_dispatch_layout_workspace_bytes(int64_t num_tokens, int top_k, int64_t num_experts) {
+  if (num_tokens < 0 || top_k < 0 || num_experts < 0) return -1;
+  return mgg::layout_chunks(num_tokens * top_k) * num_experts * (int64_t)sizeof(int32_t);
+}
+
+int mgg_dispatch_layout(const void* topk_idx, int idx_type, int64_t num_tokens, int top_k,
+                        int64_t num_experts, int32_t* counts, int32_t* offsets,
+                        int32_t* slot_position, int32_t* token_index, int32_t* row_assignment,
+                        void* workspace, int64_t workspace_bytes, void* stream) {
+  mgg::clear_error();
+  if (idx_type != MGG_INT32 && idx_type != MGG_INT64)
+    return set_error(MGG_ERR_INVALID, "idx_type must be MGG_INT32 or MGG_INT64");
+  if (num_tokens < 0 || top_k < 0 || num_experts < 0)
+    return set_error(MGG_ERR_INVALID, "sizes must be >= 0");
+  if (num_experts > mgg::kMaxLayoutExperts)
+    return set_error(MGG_ERR_UNSUPPORTED, "the dispatch layout supports at most 8192 experts");
+  const int64_t A = num_tokens * top_k;
+  if (A >= ((int64_t)1 << 31)) return set_error(MGG_ERR_UNSUPPORTED, "num_tokens * top_k must be < 2^31");
+  if (workspace_bytes < mgg_dispatch_layout_workspace_bytes(num_tokens, top_k, num_experts))
+    return set_error(MGG_ERR_INVALID, "workspace smaller than mgg_dispatch_layout_workspace_bytes");
+  if (offsets == nullptr || (num_experts > 0 && counts == nullptr))
+    return set_error(MGG_ERR_INVALID, "null counts/offsets");
+  if (A > 0 && (topk_idx == nullptr || slot_position == nullptr || token_index == nullptr ||
+                row_assignment == nullptr || (num_experts > 0 && workspace == nullptr)))
+    return set_error(MGG_ERR_INVALID, "null index or output pointer");
+  return mgg::launch_dispatch_layout(topk_idx, idx_type, num_tokens, top_k, (int32_t)num_experts,
+                                     counts, offsets, slot_position, token_index, row_assignment,
+                                     static_cast<int32_t*>(workspace),
+                                     static_cast<hipStream_t>(stream));
+}
+
+int mgg_gather_rows(int dtype, const void* x, int64_t ld_x, const int32_t* token_index,
+                    const int32_t* num_rows, int64_t max_rows, int64_t hidden, void* out,
+                    int64_t ld_out, void* stream) {
+  mgg::clear_error();
+  if (dtype != MGG_DTYPE_BF16 && dtype != MGG_DTYPE_FP16)
+    return set_error(MGG_ERR_UNSUPPORTED, "dtype must be MGG_DTYPE_BF16 or MGG_DTYPE_FP16");
+  if (max_rows < 0 || hidden < 0) return set_error(MGG_ERR_INVALID, "sizes must be >= 0");
+  if (max_rows == 0 || hidden == 0) return MGG_OK;
+  if (ld_x < hidden || ld_out < hidden)
+    return set_error(MGG_ERR_INVALID, "leading dimensions smaller than the row length");
+  if (x == nullptr || token_index == nullptr || out == nullptr)
+    return set_error(MGG_ERR_INVALID, "null pointer");
+  return mgg::launch_gather_rows(x, ld_x, token_index, num_rows, max_rows, hidden, 2, out, ld_out,
+                                 static_cast<hipStream_t>(stream));
+}
+
+int mgg_combine_rows(int dtype, const void* y, int64_t ld_y, const int32_t* slot_position,
+                     const float* weights, int64_t num_tokens, int top_k, int64_t hidden,
+                     void* out, int64_t ld_out, void* stream) {
+  mgg::clear_error();
+  if (dtype != MGG_DTYPE_BF16 && dtype != MGG_DTYPE_FP16)
+    return set_error(MGG_ERR_UNSUPPORTED, "dtype must be MGG_DTYPE_BF16 or MGG_DTYPE_FP16");
+  if (num_tokens < 0 || top_k < 0 || hidden < 0)
+    return set_error(MGG_ERR_INVALID, "sizes must be >= 0");
+  if (num_tokens == 0 || hidden == 0) return MGG_OK;
+  if (ld_out < hidden || (top_k > 0 && ld_y < hidden))
+    return set_error(MGG_ERR_INVALID, "leading dimensions smaller than the row length");
+  if (out == nullptr || (top_k > 0 && (y == nullptr || slot_position == nullptr || weights == nullptr)))
+    return set_error(MGG_ERR_INVALID, "null pointer");
+  return mgg::launch_combine_rows(dtype, y, ld_y, slot_position, weights, num_tokens, top_k,
+                                  hidden, out, ld_out, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -77,6 +77,14 @@ struct IntConst {
   static constexpr int value = V;
 };
 
+// Fused epilogues (element-wise on the fp32 accumulator, before rounding).
+__device__ __forceinline__ float gelu_erf(float x) {  // torch.nn.functional.gelu, exact form
+  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+}
+__device__ __forceinline__ float silu_mul(float gate, float up) {  // silu(gate) * up
+  return gate / (1.0f + expf(-gate)) * up;
+}
+
 // Per-expert tile prefix of the derived queue, built in LDS by the whole
 // workgroup: prefix[e] = sum_{j<e} ceil(max(off[j+1]-off[j],0)/BM) * n_tiles.
 // Returns the queue length W = prefix[E].  Same counts as
@@ -124,9 +132,9 @@ __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_pr
   return s_prefix[E];
 }
 
-// Cooperative zero fill of C[M, N] (the empty-queue case, :369-371).
-__device__ void zero_fill(const GemmParams& p) {
-  const int64_t chunks_per_row = p.n / 8;
+// Cooperative zero fill of C[M, cols] (the empty-queue case, :369-371).
+__device__ void zero_fill(const GemmParams& p, int64_t cols) {
+  const int64_t chunks_per_row = cols / 8;
   const int64_t total = p.m * chunks_per_row;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const u32x4 z = {0u, 0u, 0u, 0u};
@@ -214,7 +222,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // tile's stores, so the next tile's first DMA latency hides behind the
 // epilogue; in atomic mode the ticket of the next tile is taken early in the
 // current one.  `first` is this worker's first item (a ticket in atomic mode).
-template <int BM, int BN, int SBK, int NSTAGE, int NW, class T>
+template <int BM, int BN, int SBK, int NSTAGE, int NW, class T, int EPI>
 __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32_t first,
                                            int n_tiles, const int32_t* s_prefix,
                                            const int32_t* s_offs, int32_t* s_item, uint8_t* lds) {
@@ -538,7 +546,11 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   };
 
   // ---- epilogue: acc[i][j] register r holds D[n][m] of the 32x32 block with
-  // n = 8*(r/4) + 4*(lane/32) + r%4, m = lane%32 (D = C^T).
+  // n = 8*(r/4) + 4*(lane/32) + r%4, m = lane%32 (D = C^T).  With the SwiGLU
+  // epilogue B's columns come interleaved in groups of 64 (32 gate columns,
+  // then the 32 up columns of the same outputs), so a wave's two 32-column
+  // blocks are gate and up of the same 32 outputs and C has N/2 columns.
+  static_assert(EPI != kEpiSwiglu || kNB == 2, "SwiGLU needs two 32-column blocks per wave");
   auto epilogue = [&](const Coords& c) {
 #pragma unroll
     for (int j = 0; j < kMB; ++j) {
@@ -546,16 +558,37 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
       const int64_t grow = c.row_base + m;
       const bool row_ok = m < c.rows_valid && grow >= 0 && grow <= last_row;
       uint16_t* crow = p.c + grow * p.ldc;
-#pragma unroll
-      for (int i = 0; i < kNB; ++i) {
+      if constexpr (EPI == kEpiSwiglu) {
+        const int64_t f0 = (c.n0 + wn * (BN / kWN)) / 2;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int64_t n = c.n0 + wn * (BN / kWN) + 32 * i + 8 * g + 4 * half;
-          if (row_ok && n < p.n) {
+          const int64_t f = f0 + 8 * g + 4 * half;
+          if (row_ok && f < p.n / 2) {
+            float y[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) y[q] = silu_mul(acc[0][j][4 * g + q], acc[1][j][4 * g + q]);
             u32x2 v;
-            v[0] = T::pack(acc[i][j][4 * g + 0], acc[i][j][4 * g + 1]);
-            v[1] = T::pack(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
-            *reinterpret_cast<u32x2*>(crow + n) = v;
+            v[0] = T::pack(y[0], y[1]);
+            v[1] = T::pack(y[2], y[3]);
+            *reinterpret_cast<u32x2*>(crow + f) = v;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < kNB; ++i) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int64_t n = c.n0 + wn * (BN / kWN) + 32 * i + 8 * g + 4 * half;
+            if (row_ok && n < p.n) {
+              float y[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                y[q] = EPI == kEpiGelu ? gelu_erf(acc[i][j][4 * g + q]) : acc[i][j][4 * g + q];
+              u32x2 v;
+              v[0] = T::pack(y[0], y[1]);
+              v[1] = T::pack(y[2], y[3]);
+              *reinterpret_cast<u32x2*>(crow + n) = v;
+            }
           }
         }
       }
@@ -629,7 +662,7 @@ constexpr bool offsets_in_lds() {
 // NW waves per workgroup (4: one per SIMD; 8: two per SIMD, so one wave's
 // memory and barrier stalls are filled by the other's MFMAs).  Waves form a
 // 2 x NW/2 grid over the tile.
-template <int BM, int BN, int SBK, int NSTAGE, int NW, class T>
+template <int BM, int BN, int SBK, int NSTAGE, int NW, class T, int EPI>
 __global__ __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64),
                           amdgpu_waves_per_eu(NW / 4, NW / 4))) void
 grouped_gemm_kernel(GemmParams p) {
@@ -651,7 +684,7 @@ grouped_gemm_kernel(GemmParams p) {
                         : derive_prefix<BM, NT>(p, n_tiles, s_prefix, kOffsLds ? s_offs : nullptr,
                                                 s_scan);
   if (W == 0) {
-    zero_fill(p);
+    zero_fill(p, EPI == kEpiSwiglu ? p.n / 2 : p.n);
     return;
   }
 
@@ -670,7 +703,7 @@ grouped_gemm_kernel(GemmParams p) {
     first = s_item;
     __syncthreads();
   }
-  run_worker<BM, BN, SBK, NSTAGE, NW, T>(p, W, first, n_tiles, s_prefix,
+  run_worker<BM, BN, SBK, NSTAGE, NW, T, EPI>(p, W, first, n_tiles, s_prefix,
                                          (kOffsLds && p.num_work < 0) ? s_offs : nullptr,
                                          &s_item, lds);
   if (!p.atomic) return;
@@ -691,38 +724,59 @@ __global__ void zero_i32_kernel(int32_t* ptr, int count) {
   for (int i = threadIdx.x; i < count; i += blockDim.x) ptr[i] = 0;
 }
 
-template <class T>
+template <class T, int EPI>
 int launch_typed(int block_m, int block_n, const GemmParams& p, int workers, hipStream_t stream) {
-#define MGG_CASE(BM_, BN_, SBK_, NS_, NW_)                                                 \
-  if (block_m == BM_ && block_n == BN_) {                                                 \
-    hipLaunchKernelGGL((grouped_gemm_kernel<BM_, BN_, SBK_, NS_, NW_, T>), dim3(workers), \
-                       dim3(NW_ * 64), 0, stream, p);                                      \
-    return MGG_OK;                                                                         \
+#define MGG_CASE(BM_, BN_, SBK_, NS_, NW_)                                                      \
+  if (block_m == BM_ && block_n == BN_) {                                                      \
+    hipLaunchKernelGGL((grouped_gemm_kernel<BM_, BN_, SBK_, NS_, NW_, T, EPI>), dim3(workers), \
+                       dim3(NW_ * 64), 0, stream, p);                                           \
+    return MGG_OK;                                                                              \
   }
   // (tile, K per stage, LDS stages, waves): 128-byte A rows (64-wide K
-  // stages), as many stages as the LDS budget holds.
+  // stages), as many stages as the LDS budget holds.  Fused epilogues are
+  // compiled for the 256x256 and 128x128 tiles (two 32-column blocks per wave).
   MGG_CASE(256, 256, MGG_SBK256, MGG_NS256, MGG_NW256)
-  MGG_CASE(256, 128, 64, 3, 4)
-  MGG_CASE(128, 256, 64, 3, 4)
   MGG_CASE(128, 128, 64, 4, 4)
-  MGG_CASE(128, 64, 64, 4, 4)
-  MGG_CASE(64, 128, 64, 4, 4)
-  MGG_CASE(64, 64, 64, 4, 4)
-  MGG_CASE(256, 64, 64, 3, 4)
-  MGG_CASE(64, 256, 64, 3, 4)
+  if constexpr (EPI == kEpiNone) {
+    MGG_CASE(256, 128, 64, 3, 4)
+    MGG_CASE(128, 256, 64, 3, 4)
+    MGG_CASE(128, 64, 64, 4, 4)
+    MGG_CASE(64, 128, 64, 4, 4)
+    MGG_CASE(64, 64, 64, 4, 4)
+    MGG_CASE(256, 64, 64, 3, 4)
+    MGG_CASE(64, 256, 64, 3, 4)
+  }
 #undef MGG_CASE
-  return set_error(MGG_ERR_UNSUPPORTED, "block_m/block_n must each be one of 64, 128, 256");
+  return set_error(MGG_ERR_UNSUPPORTED, EPI == kEpiNone
+                                            ? "block_m/block_n must each be one of 64, 128, 256"
+                                            : "fused epilogues need block_m == block_n in {128, 256}");
+}
+
+template <class T>
+int launch_epi(int epilogue, int block_m, int block_n, const GemmParams& p, int workers,
+               hipStream_t stream) {
+  switch (epilogue) {
+    case kEpiNone: return launch_typed<T, kEpiNone>(block_m, block_n, p, workers, stream);
+    case kEpiGelu: return launch_typed<T, kEpiGelu>(block_m, block_n, p, workers, stream);
+    case kEpiSwiglu: return launch_typed<T, kEpiSwiglu>(block_m, block_n, p, workers, stream);
+    default: return set_error(MGG_ERR_INVALID, "unknown epilogue");
+  }
 }
 
 }  // namespace
 
-int launch_grouped_gemm(int dtype, int block_m, int block_n, const GemmParams& p, int workers,
-                        hipStream_t stream) {
+bool epilogue_supported(int epilogue, int block_m, int block_n) {
+  if (epilogue == kEpiNone) return true;
+  return block_m == block_n && (block_m == 128 || block_m == 256);
+}
+
+int launch_grouped_gemm(int dtype, int epilogue, int block_m, int block_n, const GemmParams& p,
+                        int workers, hipStream_t stream) {
   int rc;
   if (dtype == MGG_DTYPE_BF16)
-    rc = launch_typed<Bf16>(block_m, block_n, p, workers, stream);
+    rc = launch_epi<Bf16>(epilogue, block_m, block_n, p, workers, stream);
   else if (dtype == MGG_DTYPE_FP16)
-    rc = launch_typed<F16>(block_m, block_n, p, workers, stream);
+    rc = launch_epi<F16>(epilogue, block_m, block_n, p, workers, stream);
   else
     return set_error(MGG_ERR_UNSUPPORTED, "dtype must be MGG_DTYPE_BF16 or MGG_DTYPE_FP16");
   if (rc != MGG_OK) return rc;

@@ -17,6 +17,17 @@ void clear_error();
 // Largest expert count whose per-expert tile prefix fits in LDS.
 constexpr int kMaxLdsExpertsGemm = 2048;
 constexpr int kMaxLdsExpertsQueue = 8192;
+// Dispatch layout: assignments per chunk (one histogram row each) and the
+// largest expert count whose per-chunk counters fit in LDS.
+constexpr int kLayoutChunk = 1024;
+constexpr int kMaxLayoutExperts = 8192;
+
+// Fused GEMM epilogues (values of MGG_EPI_* in mgg.h).
+constexpr int kEpiNone = 0;
+constexpr int kEpiGelu = 1;
+constexpr int kEpiSwiglu = 2;
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Launch arguments of the grouped-GEMM kernels.  Element strides; byte
 // pointers so one struct serves every element type.
@@ -38,16 +49,20 @@ struct GemmParams {
   int64_t ldb_e;
   int64_t ldb_k;
   int64_t ldc;
+  const float* a_scale;  // fp8 only: one scale per row of A
+  const float* b_scale;  // fp8 only: one scale per (expert, column of B), [E, N]
   int32_t num_experts;
   int32_t num_work;  // < 0: derive the queue from the offsets on the device
   int32_t atomic;
   int32_t remap_xcd;
 };
 
-// Launches the grouped GEMM for one (dtype, block_m, block_n) on `stream`
-// with `workers` workgroups.  Returns MGG_OK or an error code.
-int launch_grouped_gemm(int dtype, int block_m, int block_n, const GemmParams& p, int workers,
-                        hipStream_t stream);
+// Launches the grouped GEMM for one (dtype, epilogue, block_m, block_n) on
+// `stream` with `workers` workgroups.  Returns MGG_OK or an error code.
+int launch_grouped_gemm(int dtype, int epilogue, int block_m, int block_n, const GemmParams& p,
+                        int workers, hipStream_t stream);
+// Whether a fused epilogue is compiled for this tile shape.
+bool epilogue_supported(int epilogue, int block_m, int block_n);
 
 // Zeroes `count` int32 values with a fill kernel on `stream`.
 int launch_zero_i32(int32_t* ptr, int count, hipStream_t stream);
@@ -58,5 +73,18 @@ int launch_offsets_from_counts(const void* counts, int counts_type, int64_t num_
 int launch_build_work_queue(const int32_t* offsets, int32_t num_experts, int64_t n_size,
                             int block_m, int block_n, int32_t* we, int32_t* wm, int32_t* wn,
                             int32_t num_work, hipStream_t stream);
+
+// Dispatch layout (three kernels; `hist` holds layout_chunks(T*k) * E int32).
+int64_t layout_chunks(int64_t assignments);
+int launch_dispatch_layout(const void* topk_idx, int idx_type, int64_t num_tokens, int top_k,
+                           int32_t num_experts, int32_t* counts, int32_t* offsets,
+                           int32_t* slot_pos, int32_t* token_index, int32_t* row_assign,
+                           int32_t* hist, hipStream_t stream);
+int launch_gather_rows(const void* x, int64_t ld_x, const int32_t* token_index,
+                       const int32_t* rows_ptr, int64_t rows_max, int64_t hidden, int elem_bytes,
+                       void* out, int64_t ld_out, hipStream_t stream);
+int launch_combine_rows(int dtype, const void* y, int64_t ld_y, const int32_t* slot_pos,
+                        const float* weight, int64_t num_tokens, int top_k, int64_t hidden,
+                        void* out, int64_t ld_out, hipStream_t stream);
 
 }  // namespace mgg

@@ -1,0 +1,329 @@
+// Token <-> expert-row movement around the grouped GEMM (one GPU's share):
+//   * dispatch layout: per-expert counts, offsets and a stable position for
+//     every (token, slot) assignment in the expert-major row order.  This is
+//     what the reference builds with sort / bincount / cumsum / inv_perm
+//     (src/train_moe_baseline.py:219-237) and what DeepEP's layout kernel
+//     counts per expert (third-party DeepEP csrc/kernels/layout.cu:10-121);
+//   * row gather into that order (train:224, grouped_tokens = tokens[perm]);
+//   * gate-weighted combine back to token order (train:246 + :340-341,
+//     out += y[inv_perm] * gate, summed over the top-k slots).
+// All are integer / byte-movement kernels: the layout kernels are latency
+// bound, gather and combine are HBM bound.
+#include "mgg.h"
+#include "mgg_internal.h"
+
+namespace mgg {
+namespace {
+
+constexpr int kLayoutThreads = 256;
+
+// Pass 1: per-chunk expert histogram (LDS atomics), one row of `hist` per
+// chunk of kLayoutChunk consecutive assignments.
+template <class In>
+__global__ void __launch_bounds__(kLayoutThreads)
+layout_count_kernel(const In* idx, int64_t A, int32_t E, int32_t* hist) {
+  extern __shared__ int32_t s_h[];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += kLayoutThreads) s_h[e] = 0;
+  __syncthreads();
+  const int64_t a0 = (int64_t)blockIdx.x * kLayoutChunk;
+  for (int i = tid; i < kLayoutChunk; i += kLayoutThreads) {
+    const int64_t a = a0 + i;
+    if (a < A) {
+      const int64_t e = (int64_t)idx[a];
+      if (e >= 0 && e < E) atomicAdd(&s_h[e], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += kLayoutThreads) hist[(int64_t)blockIdx.x * E + e] = s_h[e];
+}
+
+constexpr int kLayoutScanThreads = 1024;
+
+// Pass 2 (one workgroup): offsets[e] = sum of counts of experts below e;
+// hist[b][e] becomes the first position of chunk b's assignments to e
+// (offsets[e] + those of chunks before b), counts[e] the total.
+__global__ void __launch_bounds__(kLayoutScanThreads)
+layout_scan_kernel(int32_t* hist, int32_t nb, int32_t E, int32_t* counts, int32_t* offsets) {
+  __shared__ int32_t s_scan[kLayoutScanThreads];
+  const int tid = threadIdx.x;
+  const int per = (E + kLayoutScanThreads - 1) / kLayoutScanThreads;
+  const int e0 = tid * per;
+  // Within-expert exclusive prefix over chunks; totals per expert.
+  int32_t local = 0;
+  for (int i = 0; i < per; ++i) {
+    const int e = e0 + i;
+    if (e < E) {
+      int32_t run = 0;
+      for (int b = 0; b < nb; ++b) {
+        int32_t* h = hist + (int64_t)b * E + e;
+        const int32_t c = *h;
+        *h = run;
+        run += c;
+      }
+      counts[e] = run;
+      local += run;
+    }
+  }
+  s_scan[tid] = local;
+  __syncthreads();
+  for (int d = 1; d < kLayoutScanThreads; d <<= 1) {
+    const int32_t add = tid >= d ? s_scan[tid - d] : 0;
+    __syncthreads();
+    s_scan[tid] += add;
+    __syncthreads();
+  }
+  int32_t base = s_scan[tid] - local;
+  for (int i = 0; i < per; ++i) {
+    const int e = e0 + i;
+    if (e < E) {
+      offsets[e] = base;
+      for (int b = 0; b < nb; ++b) hist[(int64_t)b * E + e] += base;
+      base += counts[e];
+    }
+  }
+  if (tid == kLayoutScanThreads - 1) offsets[E] = s_scan[kLayoutScanThreads - 1];
+}
+
+// Pass 3 (one wave per chunk, 64 assignments at a time in order): an
+// assignment's position is its chunk's base for its expert plus the number of
+// earlier assignments of the chunk to the same expert, so positions are stable
+// (assignment order within each expert).  Lanes sharing an expert are grouped
+// with ballots, one round per distinct expert in the 64.
+template <class In>
+__global__ void __launch_bounds__(64)
+layout_scatter_kernel(const In* idx, int64_t A, int32_t top_k, int32_t E, const int32_t* hist,
+                      int32_t* slot_pos, int32_t* token_index, int32_t* row_assign) {
+  extern __shared__ int32_t s_base[];
+  const int lane = threadIdx.x;
+  for (int e = lane; e < E; e += 64) s_base[e] = hist[(int64_t)blockIdx.x * E + e];
+  __syncthreads();
+  const int64_t a0 = (int64_t)blockIdx.x * kLayoutChunk;
+  for (int t0 = 0; t0 < kLayoutChunk; t0 += 64) {
+    const int64_t a = a0 + t0 + lane;
+    if (a0 + t0 >= A) break;  // uniform
+    int32_t e = -1;
+    if (a < A) {
+      const int64_t v = (int64_t)idx[a];
+      e = (v >= 0 && v < E) ? (int32_t)v : -1;
+    }
+    const bool valid = e >= 0;
+    uint64_t todo = __ballot(valid);
+    int32_t rank = 0;
+    bool last = false;
+    while (todo != 0) {
+      const int leader = __builtin_ctzll(todo);
+      const int32_t el = __builtin_amdgcn_readlane(e, leader);
+      const bool mine = valid && e == el;
+      const uint64_t m = __ballot(mine);
+      if (mine) {
+        rank = __builtin_popcountll(m & ((1ull << lane) - 1ull));
+        last = lane == 63 - __builtin_clzll(m);
+      }
+      todo &= ~m;
+    }
+    if (valid) {
+      const int32_t pos = s_base[e] + rank;
+      slot_pos[a] = pos;
+      token_index[pos] = (int32_t)(a / top_k);
+      row_assign[pos] = (int32_t)a;
+    } else if (a < A) {
+      slot_pos[a] = -1;
+    }
+    __syncthreads();  // every lane has read its base before the bases move on
+    if (valid && last) s_base[e] += rank + 1;
+    __syncthreads();
+  }
+}
+
+constexpr int kRowThreads = 256;
+
+// out[p, :] = x[token_index[p], :] for p < offsets[E] (read on the device, so
+// the host never waits for the row count).  VEC: 16-byte chunks when every
+// row start and the row length allow it, else one element at a time.
+template <bool VEC>
+__global__ void __launch_bounds__(kRowThreads)
+gather_rows_kernel(const uint8_t* x, int64_t ld_x, const int32_t* token_index,
+                   const int32_t* rows_ptr, int64_t rows_max, int64_t row_bytes, int elem,
+                   uint8_t* out, int64_t ld_out) {
+  const int64_t rows = rows_ptr != nullptr ? (int64_t)*rows_ptr : rows_max;
+  const int64_t n = rows < rows_max ? rows : rows_max;
+  for (int64_t p = blockIdx.x; p < n; p += gridDim.x) {
+    const int64_t t = token_index[p];
+    const uint8_t* src = x + t * ld_x * elem;
+    uint8_t* dst = out + p * ld_out * elem;
+    if (VEC) {
+      for (int64_t c = threadIdx.x; c < row_bytes / 16; c += kRowThreads)
+        reinterpret_cast<uint4*>(dst)[c] = reinterpret_cast<const uint4*>(src)[c];
+    } else {
+      for (int64_t c = threadIdx.x; c < row_bytes / 2; c += kRowThreads)
+        reinterpret_cast<uint16_t*>(dst)[c] = reinterpret_cast<const uint16_t*>(src)[c];
+    }
+  }
+}
+
+template <class T>
+struct Elem;
+template <>
+struct Elem<__bf16> {
+  static __device__ __forceinline__ float load(uint16_t v) {
+    return __uint_as_float((uint32_t)v << 16);
+  }
+  static __device__ __forceinline__ uint16_t store(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
+  }
+};
+template <>
+struct Elem<_Float16> {
+  static __device__ __forceinline__ float load(uint16_t v) {
+    return (float)__builtin_bit_cast(_Float16, v);
+  }
+  static __device__ __forceinline__ uint16_t store(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+};
+
+// out[t, :] = sum_j weight[t, j] * y[slot_pos[t, j], :] over the slots with a
+// position (masked slots contribute nothing; a token with none gets zeros).
+// fp32 accumulation in slot order, one rounding to the output type.
+template <class T, bool VEC>
+__global__ void __launch_bounds__(kRowThreads)
+combine_rows_kernel(const uint16_t* y, int64_t ld_y, const int32_t* slot_pos,
+                    const float* weight, int64_t T_tokens, int32_t top_k, int64_t hidden,
+                    uint16_t* out, int64_t ld_out) {
+  for (int64_t t = blockIdx.x; t < T_tokens; t += gridDim.x) {
+    uint16_t* dst = out + t * ld_out;
+    if (VEC) {
+      for (int64_t c = threadIdx.x; c < hidden / 8; c += kRowThreads) {
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < top_k; ++j) {
+          const int32_t pos = slot_pos[t * top_k + j];
+          if (pos < 0) continue;
+          const float w = weight[t * top_k + j];
+          const uint4 v = reinterpret_cast<const uint4*>(y + (int64_t)pos * ld_y)[c];
+          const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc[2 * q] += w * Elem<T>::load((uint16_t)(words[q] & 0xFFFFu));
+            acc[2 * q + 1] += w * Elem<T>::load((uint16_t)(words[q] >> 16));
+          }
+        }
+        uint4 o;
+        uint32_t* ow = reinterpret_cast<uint32_t*>(&o);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          ow[q] = (uint32_t)Elem<T>::store(acc[2 * q]) |
+                  ((uint32_t)Elem<T>::store(acc[2 * q + 1]) << 16);
+        reinterpret_cast<uint4*>(dst)[c] = o;
+      }
+    } else {
+      for (int64_t c = threadIdx.x; c < hidden; c += kRowThreads) {
+        float acc = 0.f;
+        for (int j = 0; j < top_k; ++j) {
+          const int32_t pos = slot_pos[t * top_k + j];
+          if (pos < 0) continue;
+          acc += weight[t * top_k + j] * Elem<T>::load(y[(int64_t)pos * ld_y + c]);
+        }
+        dst[c] = Elem<T>::store(acc);
+      }
+    }
+  }
+}
+
+int grid_for(int64_t rows) {
+  const int64_t g = rows < 1 ? 1 : rows;
+  return (int)(g > 65536 ? 65536 : g);
+}
+
+}  // namespace
+
+int64_t layout_chunks(int64_t assignments) {
+  return (assignments + kLayoutChunk - 1) / kLayoutChunk;
+}
+
+int launch_dispatch_layout(const void* topk_idx, int idx_type, int64_t num_tokens, int top_k,
+                           int32_t num_experts, int32_t* counts, int32_t* offsets,
+                           int32_t* slot_pos, int32_t* token_index, int32_t* row_assign,
+                           int32_t* hist, hipStream_t stream) {
+  const int64_t A = num_tokens * top_k;
+  const int64_t nb = layout_chunks(A);
+  const size_t lds = (size_t)num_experts * sizeof(int32_t);
+  if (nb > 0) {
+    if (idx_type == MGG_INT64)
+      hipLaunchKernelGGL(layout_count_kernel<int64_t>, dim3((unsigned)nb), dim3(kLayoutThreads),
+                         lds, stream, (const int64_t*)topk_idx, A, num_experts, hist);
+    else
+      hipLaunchKernelGGL(layout_count_kernel<int32_t>, dim3((unsigned)nb), dim3(kLayoutThreads),
+                         lds, stream, (const int32_t*)topk_idx, A, num_experts, hist);
+    if (hipError_t err = hipGetLastError(); err != hipSuccess)
+      return hip_error(err, "layout count launch");
+  }
+  hipLaunchKernelGGL(layout_scan_kernel, dim3(1), dim3(kLayoutScanThreads), 0, stream, hist,
+                     (int32_t)nb, num_experts, counts, offsets);
+  if (hipError_t err = hipGetLastError(); err != hipSuccess)
+    return hip_error(err, "layout scan launch");
+  if (nb > 0) {
+    if (idx_type == MGG_INT64)
+      hipLaunchKernelGGL(layout_scatter_kernel<int64_t>, dim3((unsigned)nb), dim3(64), lds, stream,
+                         (const int64_t*)topk_idx, A, top_k, num_experts, hist, slot_pos,
+                         token_index, row_assign);
+    else
+      hipLaunchKernelGGL(layout_scatter_kernel<int32_t>, dim3((unsigned)nb), dim3(64), lds, stream,
+                         (const int32_t*)topk_idx, A, top_k, num_experts, hist, slot_pos,
+                         token_index, row_assign);
+    if (hipError_t err = hipGetLastError(); err != hipSuccess)
+      return hip_error(err, "layout scatter launch");
+  }
+  return MGG_OK;
+}
+
+int launch_gather_rows(const void* x, int64_t ld_x, const int32_t* token_index,
+                       const int32_t* rows_ptr, int64_t rows_max, int64_t hidden, int elem_bytes,
+                       void* out, int64_t ld_out, hipStream_t stream) {
+  if (rows_max <= 0 || hidden <= 0) return MGG_OK;
+  const int64_t row_bytes = hidden * elem_bytes;
+  const bool vec = row_bytes % 16 == 0 && (ld_x * elem_bytes) % 16 == 0 &&
+                   (ld_out * elem_bytes) % 16 == 0 && aligned16(x) && aligned16(out);
+  if (vec)
+    hipLaunchKernelGGL(gather_rows_kernel<true>, dim3(grid_for(rows_max)), dim3(kRowThreads), 0,
+                       stream, (const uint8_t*)x, ld_x, token_index, rows_ptr, rows_max, row_bytes,
+                       elem_bytes, (uint8_t*)out, ld_out);
+  else
+    hipLaunchKernelGGL(gather_rows_kernel<false>, dim3(grid_for(rows_max)), dim3(kRowThreads), 0,
+                       stream, (const uint8_t*)x, ld_x, token_index, rows_ptr, rows_max, row_bytes,
+                       elem_bytes, (uint8_t*)out, ld_out);
+  if (hipError_t err = hipGetLastError(); err != hipSuccess)
+    return hip_error(err, "gather launch");
+  return MGG_OK;
+}
+
+int launch_combine_rows(int dtype, const void* y, int64_t ld_y, const int32_t* slot_pos,
+                        const float* weight, int64_t num_tokens, int top_k, int64_t hidden,
+                        void* out, int64_t ld_out, hipStream_t stream) {
+  if (num_tokens <= 0 || hidden <= 0) return MGG_OK;
+  const bool vec = hidden % 8 == 0 && ld_y % 8 == 0 && ld_out % 8 == 0 && aligned16(y) &&
+                   aligned16(out);
+  const dim3 grid(grid_for(num_tokens)), block(kRowThreads);
+  const uint16_t* yy = (const uint16_t*)y;
+  uint16_t* oo = (uint16_t*)out;
+  if (dtype == MGG_DTYPE_BF16) {
+    if (vec)
+      hipLaunchKernelGGL((combine_rows_kernel<__bf16, true>), grid, block, 0, stream, yy, ld_y,
+                         slot_pos, weight, num_tokens, top_k, hidden, oo, ld_out);
+    else
+      hipLaunchKernelGGL((combine_rows_kernel<__bf16, false>), grid, block, 0, stream, yy, ld_y,
+                         slot_pos, weight, num_tokens, top_k, hidden, oo, ld_out);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((combine_rows_kernel<_Float16, true>), grid, block, 0, stream, yy, ld_y,
+                         slot_pos, weight, num_tokens, top_k, hidden, oo, ld_out);
+    else
+      hipLaunchKernelGGL((combine_rows_kernel<_Float16, false>), grid, block, 0, stream, yy, ld_y,
+                         slot_pos, weight, num_tokens, top_k, hidden, oo, ld_out);
+  }
+  if (hipError_t err = hipGetLastError(); err != hipSuccess)
+    return hip_error(err, "combine launch");
+  return MGG_OK;
+}
+
+}  // namespace mgg

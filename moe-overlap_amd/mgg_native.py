@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime this library must share)
 
 LIB_PATH = Path(__file__).resolve().parent / "libmgg.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MGG_OK = 0
 MGG_ERR_INVALID = 1
@@ -24,6 +24,9 @@ MGG_DTYPE_BF16 = 0
 MGG_DTYPE_FP16 = 1
 MGG_INT32 = 0
 MGG_INT64 = 1
+MGG_EPI_NONE = 0
+MGG_EPI_GELU = 1
+MGG_EPI_SWIGLU = 2
 
 _c_i32 = ctypes.c_int
 _c_i64 = ctypes.c_int64
@@ -49,8 +52,28 @@ _SIGNATURES = {
         _c_i32, _c_i32, _c_i32, _c_i32,  # block_m, block_n, num_workers, atomic
         _c_ptr, _c_ptr,  # work_counter, stream
     ],
+    "mgg_grouped_gemm_ex": [
+        _c_i32, _c_i32, _c_ptr, _c_ptr, _c_ptr,  # dtype, epilogue, a, b, c
+        _c_ptr, _c_i64, _c_i64, _c_i64,  # offsets, M, K, N
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,  # E, lda, ldb_e, ldb_k, ldc
+        _c_i32, _c_i32, _c_i32, _c_i32,  # block_m, block_n, num_workers, atomic
+        _c_ptr, _c_ptr,  # work_counter, stream
+    ],
+    "mgg_dispatch_layout": [
+        _c_ptr, _c_i32, _c_i64, _c_i32, _c_i64,  # topk_idx, idx_type, T, top_k, E
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,  # counts, offsets, slot_pos, token_index, row_assign
+        _c_ptr, _c_i64, _c_ptr,  # workspace, workspace_bytes, stream
+    ],
+    "mgg_gather_rows": [
+        _c_i32, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr,
+    ],
+    "mgg_combine_rows": [
+        _c_i32, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i32, _c_i64, _c_ptr, _c_i64, _c_ptr,
+    ],
 }
-EXPORTED = tuple(_SIGNATURES) + ("mgg_last_error",)
+# entry points whose return value is not a status code
+_RESTYPES = {"mgg_dispatch_layout_workspace_bytes": ([_c_i64, _c_i32, _c_i64], _c_i64)}
+EXPORTED = tuple(_SIGNATURES) + tuple(_RESTYPES) + ("mgg_last_error",)
 
 _lib = None
 
@@ -78,6 +101,10 @@ def lib() -> ctypes.CDLL:
         fn = getattr(handle, name)
         fn.argtypes = argtypes
         fn.restype = _c_i32
+    for name, (argtypes, restype) in _RESTYPES.items():
+        fn = getattr(handle, name)
+        fn.argtypes = argtypes
+        fn.restype = restype
     handle.mgg_last_error.argtypes = []
     handle.mgg_last_error.restype = ctypes.c_char_p
     version = handle.mgg_abi_version()

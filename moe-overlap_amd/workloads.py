@@ -67,6 +67,60 @@ def topk_counts(tokens: int, experts: int, top_k: int, softmax: bool = False) ->
     return torch.bincount(idx.flatten(), minlength=experts).to(torch.int32)
 
 
+def topk_routing(tokens: int, experts: int, top_k: int, softmax: bool = True):
+    """(topk_idx int64 [T, k], topk_weight fp32 [T, k]) of top-k routing on
+    N(0,1) logits (torch seed 0, CPU generator), weights the softmax
+    probabilities of the chosen experts as the reference's router gives them
+    (src/train_moe_baseline.py:316-317).  Same draw as topk_counts."""
+    gen = torch.Generator().manual_seed(0)
+    logits = torch.randn(tokens, experts, generator=gen)
+    probs = torch.softmax(logits, dim=-1) if softmax else logits
+    weight, idx = torch.topk(probs, top_k, dim=1)
+    return idx, weight.float()
+
+
+@dataclass
+class ExpertMlpCase:
+    """The BASELINE expert-MLP config: T tokens routed top-k over E experts,
+    hidden H, SwiGLU FFN of width F (gate|up 2F interleaved for the fused
+    epilogue), weights N(0, 1/fan_in)."""
+
+    tokens: int
+    experts: int
+    top_k: int
+    hidden: int
+    ffn: int
+    x: Optional[torch.Tensor] = None  # [T, H]
+    topk_idx: Optional[torch.Tensor] = None  # [T, k] int64
+    topk_weight: Optional[torch.Tensor] = None  # [T, k] fp32
+    w_gate: Optional[torch.Tensor] = None  # [E, H, F]
+    w_up: Optional[torch.Tensor] = None  # [E, H, F]
+    w2: Optional[torch.Tensor] = None  # [E, F, H]
+
+    @property
+    def flops(self) -> int:
+        rows = int((self.topk_idx >= 0).sum())
+        return 2 * rows * self.hidden * 2 * self.ffn + 2 * rows * self.ffn * self.hidden
+
+
+def make_expert_mlp_case(tokens: int = 8192, experts: int = 16, top_k: int = 2,
+                         hidden: int = 2048, ffn: int = 4096, device=None,
+                         dtype: torch.dtype = torch.bfloat16, seed: int = 0) -> ExpertMlpCase:
+    """Synthetic inputs of the expert-MLP config (defaults: BASELINE cfg 4)."""
+    case = ExpertMlpCase(tokens, experts, top_k, hidden, ffn)
+    idx, w = topk_routing(tokens, experts, top_k)
+    device = torch.device("cpu") if device is None else torch.device(device)
+    case.topk_idx = idx.to(device)
+    case.topk_weight = w.to(device)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    f32 = dict(generator=gen, device=device, dtype=torch.float32)
+    case.x = torch.randn(tokens, hidden, **f32).to(dtype)
+    case.w_gate = (torch.randn(experts, hidden, ffn, **f32) / math.sqrt(hidden)).to(dtype)
+    case.w_up = (torch.randn(experts, hidden, ffn, **f32) / math.sqrt(hidden)).to(dtype)
+    case.w2 = (torch.randn(experts, ffn, hidden, **f32) / math.sqrt(ffn)).to(dtype)
+    return case
+
+
 def make_case(
     name: str,
     device: Optional[torch.device] = None,
