@@ -32,7 +32,7 @@ sys.path.insert(0, str(REPO))
 METRIC = "grouped GEMM TFLOP/s + % bf16 MFMA peak, E=16 512 tok/expert K2048 N4096"
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0
-KERNEL_NAME = "grouped_gemm_kernel<256,256,64,2,8,Bf16>"
+KERNEL_NAME = "grouped_gemm_kernel<256,256,64,2,8,Bf16,0>"
 
 
 def parse_args():
@@ -92,6 +92,54 @@ def recorded_traffic(mode, workload, block_m, block_n):
 def median(xs):
     ys = sorted(xs)
     return ys[len(ys) // 2] if ys else float("nan")
+
+
+def expert_mlp_summary(dev, steps: int = 10):
+    """The BASELINE expert-MLP config (8192 tokens top-2 of 16, H 2048, SwiGLU
+    F 4096): whole forward (layout, gather, up GEMM + SwiGLU, down GEMM,
+    combine) and each launch alone, from HIP events on the current stream."""
+    import torch
+
+    import expert_mlp as mlp
+    import workloads
+
+    case = workloads.make_expert_mlp_case(device=dev)
+    w1 = mlp.interleave_gate_up(case.w_gate, case.w_up)
+    case.w_gate = case.w_up = None
+    fwd = lambda: mlp.expert_mlp_forward(case.x, case.topk_idx, case.topk_weight, w1, case.w2,
+                                         "swiglu")
+    event_times_ms(fwd, 3)
+    t_fwd = median(event_times_ms(fwd, steps))
+    lay = mlp.dispatch_layout(case.topk_idx, case.experts)
+    xp = mlp.permute_tokens(case.x, lay)
+    h = mlp._grouped_gemm_ex(xp, w1, lay.offsets, mlp._EPILOGUES["swiglu"], case.ffn, None, 256, True)
+    y = mlp._grouped_gemm_ex(h, case.w2, lay.offsets, mlp._EPILOGUES["none"], case.hidden, None, 256, True)
+    parts = {
+        "dispatch_layout": lambda: mlp.dispatch_layout(case.topk_idx, case.experts),
+        "gather": lambda: mlp.permute_tokens(case.x, lay),
+        "up_gemm_swiglu": lambda: mlp._grouped_gemm_ex(xp, w1, lay.offsets, mlp._EPILOGUES["swiglu"],
+                                                      case.ffn, None, 256, True),
+        "down_gemm": lambda: mlp._grouped_gemm_ex(h, case.w2, lay.offsets, mlp._EPILOGUES["none"],
+                                                 case.hidden, None, 256, True),
+        "combine": lambda: mlp.combine_tokens(y, lay, case.topk_weight),
+    }
+    rows = case.tokens * case.top_k
+    up_flops = 2 * rows * case.hidden * 2 * case.ffn
+    down_flops = 2 * rows * case.ffn * case.hidden
+    out = {"config": f"T={case.tokens} top-{case.top_k} of E={case.experts}, H={case.hidden}, "
+                     f"SwiGLU F={case.ffn}, bf16",
+           "forward_ms_median": round(t_fwd, 4),
+           "forward_tflops": round(case.flops / (t_fwd * 1e-3) / 1e12, 1),
+           "launch_ms_median": {}}
+    for name, fn in parts.items():
+        event_times_ms(fn, 2)
+        out["launch_ms_median"][name] = round(median(event_times_ms(fn, steps)), 4)
+    lm = out["launch_ms_median"]
+    out["up_gemm_tflops"] = round(up_flops / (lm["up_gemm_swiglu"] * 1e-3) / 1e12, 1)
+    out["down_gemm_tflops"] = round(down_flops / (lm["down_gemm"] * 1e-3) / 1e12, 1)
+    del case, w1, lay, xp, h, y
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(case, budget_s):
@@ -223,6 +271,7 @@ def main():
         tl = event_times_ms(loop, 5)
         extra["torch_loop_gpu_ms_median"] = round(median(tl), 4)
         extra["torch_loop_gpu_tflops"] = round(flops / (median(tl) * 1e-3) / 1e12, 1)
+        extra["expert_mlp"] = expert_mlp_summary(dev)
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(case, args.cpu_seconds)
 
