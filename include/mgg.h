@@ -30,6 +30,9 @@
  *                                     csrc/kernels/layout.cu:10-121)
  *   mgg_gather_rows                -> grouped_tokens = valid_tokens[perm]
  *                                     (src/train_moe_baseline.py:224)
+ *   mgg_grouped_gemm_fp8           -> no counterpart: the reference rejects
+ *                                     fp8 (src/triton_grouped_gemm.py:357-358);
+ *                                     the fp8 config of the build's baseline
  *   mgg_combine_rows               -> out[valid] = grouped_out[inv_perm] and
  *                                     out += y * gate over the top-k slots
  *                                     (src/train_moe_baseline.py:245-246, :340-341)
@@ -52,6 +55,7 @@ extern "C" {
 /* Element types of the GEMM operands. */
 #define MGG_DTYPE_BF16 0
 #define MGG_DTYPE_FP16 1
+#define MGG_DTYPE_FP8_E4M3 2 /* OCP e4m3 (float8_e4m3fn) operands, BF16 output */
 
 /* Fused GEMM epilogues (mgg_grouped_gemm_ex). */
 #define MGG_EPI_NONE 0
@@ -162,6 +166,27 @@ int mgg_grouped_gemm_ex(int dtype, int epilogue, const void* a, const void* b, v
                         int64_t n_size, int64_t num_experts, int64_t lda, int64_t ldb_e,
                         int64_t ldb_k, int64_t ldc, int block_m, int block_n, int num_workers,
                         int use_atomic_queue, int32_t* work_counter, void* stream);
+
+/*
+ * fp8 grouped GEMM with per-token and per-channel scales:
+ *   C[r, n] = a_scale[r] * b_scale[e, n] * sum_k A[r, k] * B[e, n, k]
+ * for rows r of expert e's range, fp32 accumulation, BF16 output.
+ *   a  [M, K]     OCP e4m3 bytes, row stride lda
+ *   b  [E, N, K]  OCP e4m3 bytes, K contiguous (the [out, in] layout of a
+ *                 linear layer's weight), expert stride ldb_e, row stride ldb_n
+ *   a_scale [M], b_scale [E, N] (row stride N): fp32 on the device
+ *   c  [M, N]     BF16, row stride ldc
+ * Queue, schedules, work_counter and empty-queue behaviour as in
+ * mgg_grouped_gemm (queue derived on the device).  Tiles 256x128 and
+ * 128x128; K, lda, ldb_n, ldb_e multiples of 16; N, ldc multiples of 8.
+ * (Introduced with ABI version 2.)
+ */
+int mgg_grouped_gemm_fp8(const void* a, const void* b, void* c, const int32_t* expert_offsets,
+                         const float* a_scale, const float* b_scale, int64_t m_size,
+                         int64_t k_size, int64_t n_size, int64_t num_experts, int64_t lda,
+                         int64_t ldb_e, int64_t ldb_n, int64_t ldc, int block_m, int block_n,
+                         int num_workers, int use_atomic_queue, int32_t* work_counter,
+                         void* stream);
 
 /*
  * Dispatch layout of T tokens routed to top_k experts each (one GPU's share):

@@ -175,10 +175,16 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
                       int64_t n_size, int64_t num_experts, int64_t lda, int64_t ldb_e,
                       int64_t ldb_k, int64_t ldc, const int32_t* work_expert,
                       const int32_t* work_tile_m, const int32_t* work_tile_n, int64_t num_work,
-                      int block_m, int block_n, int num_workers, int use_atomic_queue,
-                      int32_t* work_counter, hipStream_t st) {
-  if (dtype != MGG_DTYPE_BF16 && dtype != MGG_DTYPE_FP16)
+                      const float* a_scale, const float* b_scale, int block_m, int block_n,
+                      int num_workers, int use_atomic_queue, int32_t* work_counter,
+                      hipStream_t st) {
+  const bool fp8 = dtype == MGG_DTYPE_FP8_E4M3;
+  if (dtype != MGG_DTYPE_BF16 && dtype != MGG_DTYPE_FP16 && !fp8)
     return set_error(MGG_ERR_UNSUPPORTED, "dtype must be MGG_DTYPE_BF16 or MGG_DTYPE_FP16");
+  if (fp8 && epilogue != MGG_EPI_NONE)
+    return set_error(MGG_ERR_UNSUPPORTED, "fp8 takes no fused epilogue");
+  if (fp8 && !((block_m == 256 && block_n == 128) || (block_m == 128 && block_n == 128)))
+    return set_error(MGG_ERR_UNSUPPORTED, "fp8 tiles are 256x128 and 128x128");
   if (epilogue != MGG_EPI_NONE && epilogue != MGG_EPI_GELU && epilogue != MGG_EPI_SWIGLU)
     return set_error(MGG_ERR_INVALID, "epilogue must be MGG_EPI_NONE, MGG_EPI_GELU or MGG_EPI_SWIGLU");
   const bool block_ok = (block_m == 64 || block_m == 128 || block_m == 256) &&
@@ -192,10 +198,13 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   if (m_size == 0 || n_size == 0) return MGG_OK;  // C has no elements
   if (k_size % 8 != 0 || n_size % 8 != 0)
     return set_error(MGG_ERR_UNSUPPORTED, "K and N must be multiples of 8");
+  if (fp8 && (k_size % 16 != 0 || lda % 16 != 0 || ldb_k % 16 != 0 || ldb_e % 16 != 0))
+    return set_error(MGG_ERR_UNSUPPORTED, "fp8: K and the A/B strides must be multiples of 16");
   if (epilogue == MGG_EPI_SWIGLU && n_size % 64 != 0)
     return set_error(MGG_ERR_UNSUPPORTED, "SwiGLU needs N (gate and up columns) a multiple of 64");
   const int64_t c_cols = epilogue == MGG_EPI_SWIGLU ? n_size / 2 : n_size;
-  if (lda < k_size || ldb_k < n_size || ldc < c_cols || ldb_e < 0)
+  // ldb_k: stride between B's rows (K rows of N values; for fp8, N rows of K values).
+  if (lda < k_size || ldb_k < (fp8 ? k_size : n_size) || ldc < c_cols || ldb_e < 0)
     return set_error(MGG_ERR_INVALID, "leading dimensions smaller than the matrix extents");
   if (lda % 8 != 0 || ldb_k % 8 != 0 || ldb_e % 8 != 0 || ldc % 8 != 0)
     return set_error(MGG_ERR_UNSUPPORTED, "strides must be multiples of 8 elements");
@@ -203,11 +212,15 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   const bool reads_ab = num_experts > 0 && k_size > 0;
   if (c == nullptr || expert_offsets == nullptr || (reads_ab && (a == nullptr || b == nullptr)))
     return set_error(MGG_ERR_INVALID, "null operand pointer");
+  if (fp8 && num_experts > 0 && (a_scale == nullptr || b_scale == nullptr))
+    return set_error(MGG_ERR_INVALID, "fp8 needs a_scale and b_scale");
   if (!aligned16(a) || !aligned16(b) || !aligned16(c))
     return set_error(MGG_ERR_UNSUPPORTED, "operand base pointers must be 16-byte aligned");
   // In-tile byte offsets are 32-bit: BM rows of A, K+8 rows of B.
   const int64_t lim = ((int64_t)1 << 31) - 4096;
-  if ((int64_t)block_m * lda * 2 + k_size * 2 >= lim || (k_size + 8) * ldb_k * 2 >= lim)
+  const int64_t es = fp8 ? 1 : 2;
+  const int64_t b_span = fp8 ? ((int64_t)block_n * ldb_k + k_size) : (k_size + 8) * ldb_k;
+  if ((int64_t)block_m * lda * es + k_size * es >= lim || b_span * es >= lim)
     return set_error(MGG_ERR_UNSUPPORTED, "row strides too large for 32-bit tile offsets");
 
   int workers = num_workers;
@@ -252,6 +265,8 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   p.ldb_e = ldb_e;
   p.ldb_k = ldb_k;
   p.ldc = ldc;
+  p.a_scale = a_scale;
+  p.b_scale = b_scale;
   p.num_experts = (int32_t)num_experts;
   p.num_work = num_work >= 0 ? (int32_t)num_work : -1;
   p.atomic = use_atomic_queue ? 1 : 0;
@@ -281,8 +296,9 @@ int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
   mgg::clear_error();
   return mgg::grouped_gemm_impl(dtype, MGG_EPI_NONE, a, b, c, expert_offsets, m_size, k_size,
                                 n_size, num_experts, lda, ldb_e, ldb_k, ldc, work_expert,
-                                work_tile_m, work_tile_n, num_work, block_m, block_n, num_workers,
-                                use_atomic_queue, work_counter, static_cast<hipStream_t>(stream));
+                                work_tile_m, work_tile_n, num_work, nullptr, nullptr, block_m,
+                                block_n, num_workers, use_atomic_queue, work_counter,
+                                static_cast<hipStream_t>(stream));
 }
 
 int mgg_grouped_gemm_ex(int dtype, int epilogue, const void* a, const void* b, void* c,
@@ -291,9 +307,25 @@ int mgg_grouped_gemm_ex(int dtype, int epilogue, const void* a, const void* b, v
                         int64_t ldb_k, int64_t ldc, int block_m, int block_n, int num_workers,
                         int use_atomic_queue, int32_t* work_counter, void* stream) {
   mgg::clear_error();
+  if (dtype == MGG_DTYPE_FP8_E4M3)
+    return set_error(MGG_ERR_UNSUPPORTED, "fp8 goes through mgg_grouped_gemm_fp8");
   return mgg::grouped_gemm_impl(dtype, epilogue, a, b, c, expert_offsets, m_size, k_size, n_size,
                                 num_experts, lda, ldb_e, ldb_k, ldc, nullptr, nullptr, nullptr, -1,
-                                block_m, block_n, num_workers, use_atomic_queue, work_counter,
+                                nullptr, nullptr, block_m, block_n, num_workers, use_atomic_queue,
+                                work_counter, static_cast<hipStream_t>(stream));
+}
+
+int mgg_grouped_gemm_fp8(const void* a, const void* b, void* c, const int32_t* expert_offsets,
+                         const float* a_scale, const float* b_scale, int64_t m_size,
+                         int64_t k_size, int64_t n_size, int64_t num_experts, int64_t lda,
+                         int64_t ldb_e, int64_t ldb_n, int64_t ldc, int block_m, int block_n,
+                         int num_workers, int use_atomic_queue, int32_t* work_counter,
+                         void* stream) {
+  mgg::clear_error();
+  return mgg::grouped_gemm_impl(MGG_DTYPE_FP8_E4M3, MGG_EPI_NONE, a, b, c, expert_offsets, m_size,
+                                k_size, n_size, num_experts, lda, ldb_e, ldb_n, ldc, nullptr,
+                                nullptr, nullptr, -1, a_scale, b_scale, block_m, block_n,
+                                num_workers, use_atomic_queue, work_counter,
                                 static_cast<hipStream_t>(stream));
 }
 

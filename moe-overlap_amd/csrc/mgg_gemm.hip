@@ -40,8 +40,19 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+
+// Operand types.  kElem: bytes per element; kMfmaK: K of one 32x32 MFMA;
+// Frag: one lane's operand of it (8 consecutive K of a row for 16-bit types,
+// 32 for fp8); kBKMajor: B is stored [E, N, K] (K contiguous) rather than
+// [E, K, N]; kScaled: the output is scaled per row of A and per (expert,
+// column of B) before rounding.  The output is 16-bit in every case.
 struct Bf16 {
-  static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+  static constexpr int kElem = 2, kMfmaK = 16;
+  static constexpr bool kBKMajor = false, kScaled = false;
+  using Frag = u32x4;
+  static __device__ __forceinline__ f32x16 mfma(Frag a, Frag b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
@@ -52,7 +63,10 @@ struct Bf16 {
 };
 
 struct F16 {
-  static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+  static constexpr int kElem = 2, kMfmaK = 16;
+  static constexpr bool kBKMajor = false, kScaled = false;
+  using Frag = u32x4;
+  static __device__ __forceinline__ f32x16 mfma(Frag a, Frag b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
@@ -60,6 +74,20 @@ struct F16 {
     f16x2 v = {(_Float16)lo, (_Float16)hi};
     return __builtin_bit_cast(uint32_t, v);
   }
+};
+
+// OCP fp8 e4m3 operands (v_mfma_f32_32x32x64_f8f6f4, both formats e4m3: lane
+// l holds row l%32, K 32*(l/32) .. +31), bf16 output.  The scaled builtin with
+// zero scale operands is the unscaled instruction.
+struct Fp8 {
+  static constexpr int kElem = 1, kMfmaK = 64;
+  static constexpr bool kBKMajor = true, kScaled = true;
+  using Frag = u32x8;
+  static __device__ __forceinline__ f32x16 mfma(Frag a, Frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+        __builtin_bit_cast(i32x8, a), __builtin_bit_cast(i32x8, b), c, 0, 0, 0, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return Bf16::pack(lo, hi); }
 };
 
 __device__ __forceinline__ u32x4 lds_load(const uint8_t* base, int off) {
@@ -225,25 +253,33 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 template <int BM, int BN, int SBK, int NSTAGE, int NW, class T, int EPI>
 __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32_t first,
                                            int n_tiles, const int32_t* s_prefix,
-                                           const int32_t* s_offs, int32_t* s_item, uint8_t* lds) {
-  constexpr int kBK = SBK;                  // K per stage
+                                           const int32_t* s_offs, int32_t* s_item, uint8_t* lds,
+                                           float* s_scale) {
+  constexpr int kBK = SBK;                  // K (elements) per stage
   constexpr int kStages = NSTAGE;           // LDS stages in rotation
-  constexpr int kSteps = kBK / 16;          // MFMA K steps per stage
-  constexpr int kARowBytes = kBK * 2;
-  constexpr int kAChunks = kBK / 8;         // 16-byte chunks per A row
+  constexpr int kE = T::kElem;              // bytes per operand element
+  constexpr int kChunkElems = 16 / kE;      // elements per 16-byte chunk
+  constexpr int kSteps = kBK / T::kMfmaK;   // MFMA K steps per stage
+  constexpr int kARowBytes = kBK * kE;
+  constexpr int kAChunks = kARowBytes / 16; // 16-byte chunks per A row
   constexpr int kARowsPerDma = 64 / kAChunks;
   constexpr int kAStage = BM * kARowBytes;  // bytes of A per stage
-  constexpr int kBStage = kBK * BN * 2;     // bytes of B per stage
-  constexpr int kBRowBytes = BN * 2;
+  constexpr int kBStage = kBK * BN * kE;    // bytes of B per stage
+  // LDS rows of B: K-major B is stored like A (BN rows of the stage's K
+  // bytes); otherwise K rows of BN 16-bit values.
+  constexpr int kBRowBytes = T::kBKMajor ? kARowBytes : BN * 2;
   constexpr int kAPerWave = BM / (NW * kARowsPerDma);  // A DMAs per wave per stage
   constexpr int kBPerWave = kBStage / (1024 * NW);     // B DMAs per wave per stage
   constexpr int kWN = NW / 2;                          // waves along N (2 along M)
   static_assert(kAPerWave >= 1 && kBPerWave >= 1, "tile too small for the wave count");
-  static_assert(kSteps == 1 || kSteps == 2 || kSteps == 4, "K per stage must be 16, 32 or 64");
+  static_assert(kSteps == 1 || kSteps == 2 || kSteps == 4, "a stage must be 1, 2 or 4 MFMA K steps");
   static_assert(kStages >= 2, "need at least two LDS stages");
   constexpr int kDmaPerStage = kAPerWave + kBPerWave;
-  constexpr int kBChunks = BN / 8;          // 16-byte chunks per B row
+  constexpr int kBChunks = kBRowBytes / 16;  // 16-byte chunks per B row
   constexpr int kBRowsPerDma = 64 / kBChunks;
+  // 16-byte chunks of one MFMA K step in a row, and of one lane's fragment.
+  constexpr int kStepChunks = T::kMfmaK * kE / 16;
+  constexpr int kFragChunks = kStepChunks / 2;
   constexpr int kMB = BM / 64;              // 32-row MFMA blocks per wave
   constexpr int kNB = BN / (32 * kWN);      // 32-col MFMA blocks per wave
   static_assert(kNB >= 1, "tile too narrow for the wave count");
@@ -312,22 +348,28 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   // Each descriptor ends exactly at the last element of its operand, so a
   // DMA past it writes zeros: rows of A past M, rows of B past K.  Rows of A
   // inside [0, M) but past this expert's count bring the next expert's data;
-  // their results are never stored.  B columns past N (edge tiles) are
-  // clamped onto the last 8 columns.  Offsets are 32-bit (the host bounds
-  // lda and ldb_k).
+  // their results are never stored.  K-major B is handled like A (rows of
+  // B past N read zeros).  N-major B columns past N (edge tiles) are clamped
+  // onto the last 8 columns.  Offsets are 32-bit (the host bounds lda and
+  // ldb_k).  ldb_k is the stride between B's rows: K rows for N-major B, N
+  // rows for K-major B.
   auto a_swz = [](int r) {
     return kAChunks == 2 ? (r >> 3) & 1 : kAChunks == 4 ? (r >> 2) & 3 : (r >> 1) & 7;
   };
   // Chunk (row, K position) moved by lane `lane` in the t-th DMA of a stage.
   auto a_row = [&](int t) { return kARowsPerDma * (wave * kAPerWave + t) + lane / kAChunks; };
-  auto a_kpos = [&](int t) { return 8 * ((lane % kAChunks) ^ a_swz(a_row(t))); };
+  auto a_kpos = [&](int t) { return kChunkElems * ((lane % kAChunks) ^ a_swz(a_row(t))); };
   auto b_krow = [&](int t) { return (wave * kBPerWave + t) * kBRowsPerDma + lane / kBChunks; };
+  // K-major B: row n of the tile and the K position of the chunk.
+  auto b_kpos = [&](int t) { return kChunkElems * ((lane % kBChunks) ^ a_swz(b_krow(t))); };
   uint32_t a_voff[kAPerWave];  // per-lane source offsets (bytes, stage 0), the same for every tile
 #pragma unroll
-  for (int t = 0; t < kAPerWave; ++t) a_voff[t] = (uint32_t)((a_row(t) * p.lda + a_kpos(t)) * 2);
-  const uint32_t b_row_bytes = (uint32_t)(p.ldb_k * 2);
+  for (int t = 0; t < kAPerWave; ++t) a_voff[t] = (uint32_t)((a_row(t) * p.lda + a_kpos(t)) * kE);
+  const uint32_t b_row_bytes = (uint32_t)(p.ldb_k * kE);
   const uint32_t lds_a0 = lds_addr(lds);
   const uint32_t lds_b0 = lds_a0 + kStages * kAStage;
+  const uint8_t* a_bytes = reinterpret_cast<const uint8_t*>(p.a);
+  const uint8_t* b_bytes = reinterpret_cast<const uint8_t*>(p.b);
 
   // The DMA state of the tile whose stages are being issued.
   i32x4 a_rsrc, b_rsrc;
@@ -335,17 +377,25 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   auto set_sources = [&](const Coords& c) {
     int64_t r0 = c.row_base;
     r0 = r0 < 0 ? 0 : (r0 > p.m ? p.m : r0);
-    const int64_t a_end = r0 < p.m ? ((p.m - 1 - r0) * p.lda + K) * 2 : 0;
-    a_rsrc = make_rsrc4(p.a + r0 * p.lda, a_end);
-    const int64_t b_end = ((K - 1) * p.ldb_k + p.n - c.n0) * 2;
-    b_rsrc = make_rsrc4(p.b + (int64_t)c.e * p.ldb_e + c.n0, b_end);
+    const int64_t a_end = r0 < p.m ? ((p.m - 1 - r0) * p.lda + K) * kE : 0;
+    a_rsrc = make_rsrc4(a_bytes + r0 * p.lda * kE, a_end);
+    if constexpr (T::kBKMajor) {
+      const int64_t b_end = c.n0 < p.n ? ((p.n - 1 - c.n0) * p.ldb_k + K) * kE : 0;
+      b_rsrc = make_rsrc4(b_bytes + ((int64_t)c.e * p.ldb_e + c.n0 * p.ldb_k) * kE, b_end);
 #pragma unroll
-    for (int t = 0; t < kBPerWave; ++t) {
-      const int k = b_krow(t);
-      const int swz = BN >= 128 ? 4 * (k & 3) : 4 * ((k >> 1) & 1);
-      int64_t col = 8 * ((lane % kBChunks) ^ swz);
-      col = c.n0 + col > p.n - 8 ? p.n - 8 - c.n0 : col;
-      b_voff[t] = (uint32_t)((k * p.ldb_k + col) * 2);
+      for (int t = 0; t < kBPerWave; ++t)
+        b_voff[t] = (uint32_t)((b_krow(t) * p.ldb_k + b_kpos(t)) * kE);
+    } else {
+      const int64_t b_end = ((K - 1) * p.ldb_k + p.n - c.n0) * 2;
+      b_rsrc = make_rsrc4(b_bytes + ((int64_t)c.e * p.ldb_e + c.n0) * 2, b_end);
+#pragma unroll
+      for (int t = 0; t < kBPerWave; ++t) {
+        const int k = b_krow(t);
+        const int swz = BN >= 128 ? 4 * (k & 3) : 4 * ((k >> 1) & 1);
+        int64_t col = 8 * ((lane % kBChunks) ^ swz);
+        col = c.n0 + col > p.n - 8 ? p.n - 8 - c.n0 : col;
+        b_voff[t] = (uint32_t)((k * p.ldb_k + col) * 2);
+      }
     }
   };
 
@@ -365,14 +415,22 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
       if (d < kAPerWave) {
         const int t = d;
         if (full) {
-          dma16(a_rsrc, a_voff[t], (uint32_t)k0 * 2u, la + t * 1024);
+          dma16(a_rsrc, a_voff[t], (uint32_t)k0 * kE, la + t * 1024);
         } else {
-          const uint32_t v = k0 + a_kpos(t) < k_size ? a_voff[t] + (uint32_t)k0 * 2u : kOutOfRange;
+          const uint32_t v = k0 + a_kpos(t) < k_size ? a_voff[t] + (uint32_t)k0 * kE : kOutOfRange;
           dma16(a_rsrc, v, 0u, la + t * 1024);
         }
       } else {
         const int t = d - kAPerWave;
-        if (full) {
+        if constexpr (T::kBKMajor) {
+          if (full) {
+            dma16(b_rsrc, b_voff[t], (uint32_t)k0 * kE, lb + t * 1024);
+          } else {
+            const uint32_t v =
+                k0 + b_kpos(t) < k_size ? b_voff[t] + (uint32_t)k0 * kE : kOutOfRange;
+            dma16(b_rsrc, v, 0u, lb + t * 1024);
+          }
+        } else if (full) {
           dma16(b_rsrc, b_voff[t], (uint32_t)k0 * b_row_bytes, lb + t * 1024);
         } else {
           const uint32_t v =
@@ -387,30 +445,59 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   // ---- fragment addresses (LDS bytes, stage 0) ----------------------------
   const int frag_row = lane & 31;
   const int half = lane >> 5;
+  // A fragment of K step kk: chunks kk*kStepChunks + half*kFragChunks + q of
+  // row frag_row (+32j rows per block, the same swizzle).
   const uint32_t a_frag0 = (uint32_t)((wm * (BM / 2) + frag_row) * kARowBytes);
-  uint32_t a_off[kSteps];  // rows 32j further are +32j*kARowBytes (same swizzle)
+  uint32_t a_off[kSteps][kFragChunks];
 #pragma unroll
   for (int kk = 0; kk < kSteps; ++kk)
-    a_off[kk] = lds_a0 + a_frag0 + (uint32_t)(((2 * kk + half) ^ a_swz(frag_row)) * 16);
+#pragma unroll
+    for (int q = 0; q < kFragChunks; ++q)
+      a_off[kk][q] = lds_a0 + a_frag0 +
+                     (uint32_t)(((kk * kStepChunks + half * kFragChunks + q) ^ a_swz(frag_row)) * 16);
   const int tg = lane >> 4, ts = lane & 15;  // transposing-read group and source lane
   const int b_row_l = 8 * (tg >> 1) + (ts >> 2);
   const int b_swz = BN >= 128 ? 4 * ((ts >> 2) & 3) : 4 * ((ts >> 3) & 1);
-  uint32_t b_off[kNB];
+  uint32_t b_off[kNB];  // N-major B: transposing-read address of block i (stage 0, K step 0)
+  uint32_t bk_off[kSteps][kFragChunks];  // K-major B: like A, rows wn*(BN/kWN) + frag_row
 #pragma unroll
   for (int i = 0; i < kNB; ++i) {
     const int n = wn * (BN / kWN) + 32 * i + 16 * (tg & 1) + 4 * (ts & 3);
     b_off[i] = lds_b0 + (uint32_t)(b_row_l * kBRowBytes + (((n >> 3) ^ b_swz) * 16) + (n & 7) * 2);
   }
+  const int b_frag_row = wn * (BN / kWN) + frag_row;
+#pragma unroll
+  for (int kk = 0; kk < kSteps; ++kk)
+#pragma unroll
+    for (int q = 0; q < kFragChunks; ++q)
+      bk_off[kk][q] = lds_b0 + (uint32_t)(b_frag_row * kBRowBytes) +
+                      (uint32_t)(((kk * kStepChunks + half * kFragChunks + q) ^ a_swz(b_frag_row)) * 16);
 
   f32x16 acc[kNB][kMB];
   // Fragments are double-buffered by the parity of the K step's global index
   // (k0/16): buffer f holds the step being multiplied while the other fills.
-  u32x4 fa[2][kMB];
-  u32x4 fb[2][kNB];
+  using Frag = typename T::Frag;
+  Frag fa[2][kMB];
+  Frag fb[2][kNB];
+  // One fragment from kFragChunks 16-byte LDS reads at byte offsets off[q] + delta.
+  auto read_rows = [&](const uint32_t* off, uint32_t delta) {
+    Frag v;
+#pragma unroll
+    for (int q = 0; q < kFragChunks; ++q) {
+      const u32x4 w = lds_load(lds, off[q] + delta - lds_a0);
+#pragma unroll
+      for (int x = 0; x < 4; ++x) v[4 * q + x] = w[x];
+    }
+    return v;
+  };
   auto read_a = [&](int f, int buf, int kk, int j) {
-    fa[f][j] = lds_load(lds, a_off[kk] + buf * kAStage + 32 * kARowBytes * j - lds_a0);
+    fa[f][j] = read_rows(a_off[kk], buf * kAStage + 32 * kARowBytes * j);
   };
   auto read_b = [&](int f, int buf, int kk, int i) {
+    if constexpr (T::kBKMajor) {
+      fb[f][i] = read_rows(bk_off[kk], buf * kBStage + 32 * kBRowBytes * i);
+      return;
+    }
     const uint32_t base = b_off[i] + buf * kBStage + 16 * kk * kBRowBytes - lds_a0;
     const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (lds_i16x4*)(lds_ptr(lds) + base));
@@ -418,7 +505,12 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
         (lds_i16x4*)(lds_ptr(lds) + base + 4 * kBRowBytes));
     const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
     const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
-    fb[f][i] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+    Frag v;
+    v[0] = l2[0];
+    v[1] = l2[1];
+    v[2] = h2[0];
+    v[3] = h2[1];
+    fb[f][i] = v;
   };
   // Half `part` of the fragments of K step kk of LDS buffer `buf`, into fragment buffer f.
   auto read_kstep = [&](int f, int buf, int kk, int part) {
@@ -511,7 +603,23 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   // All stages of the current tile; stages 0 .. min(kStages-1, nk)-1 have
   // been issued.  Returns after the last stage's fragments have been read
   // and its MFMAs issued.
-  auto main_loop = [&](bool take_ticket, int32_t& ticket) {
+  // Scaled types: the tile's row and column scales go to LDS (buffer `sb`
+  // alternates per tile, so the previous tile's epilogue may still read the
+  // other one) before the first barrier of the tile.
+  int scale_buf = 0;
+  auto main_loop = [&](const Coords& c, bool take_ticket, int32_t& ticket) {
+    if constexpr (T::kScaled) {
+      float* sc = s_scale + scale_buf * (BM + BN);
+      for (int i = tid; i < BM + BN; i += NW * 64) {
+        float v = 0.0f;
+        if (i < BM) {
+          if (i < c.rows_valid) v = p.a_scale[c.row_base + i];
+        } else if (c.n0 + (i - BM) < p.n) {
+          v = p.b_scale[(int64_t)c.e * p.n + c.n0 + (i - BM)];
+        }
+        sc[i] = v;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < kNB; ++i)
 #pragma unroll
@@ -551,10 +659,13 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   // then the 32 up columns of the same outputs), so a wave's two 32-column
   // blocks are gate and up of the same 32 outputs and C has N/2 columns.
   static_assert(EPI != kEpiSwiglu || kNB == 2, "SwiGLU needs two 32-column blocks per wave");
+  static_assert(EPI == kEpiNone || !T::kScaled, "fused epilogues are for unscaled types");
   auto epilogue = [&](const Coords& c) {
+    const float* sc = s_scale + scale_buf * (BM + BN);
 #pragma unroll
     for (int j = 0; j < kMB; ++j) {
       const int m = wm * (BM / 2) + 32 * j + frag_row;
+      const float row_scale = T::kScaled ? sc[m] : 1.0f;
       const int64_t grow = c.row_base + m;
       const bool row_ok = m < c.rows_valid && grow >= 0 && grow <= last_row;
       uint16_t* crow = p.c + grow * p.ldc;
@@ -582,8 +693,12 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
             if (row_ok && n < p.n) {
               float y[4];
 #pragma unroll
-              for (int q = 0; q < 4; ++q)
-                y[q] = EPI == kEpiGelu ? gelu_erf(acc[i][j][4 * g + q]) : acc[i][j][4 * g + q];
+              for (int q = 0; q < 4; ++q) {
+                float v = acc[i][j][4 * g + q];
+                if constexpr (T::kScaled)
+                  v *= row_scale * sc[BM + wn * (BN / kWN) + 32 * i + 8 * g + 4 * half + q];
+                y[q] = EPI == kEpiGelu ? gelu_erf(v) : v;
+              }
               u32x2 v;
               v[0] = T::pack(y[0], y[1]);
               v[1] = T::pack(y[2], y[3]);
@@ -621,7 +736,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     if (s < nk) issue_stage(issued = s);
   for (;;) {
     int32_t ticket = 0;
-    main_loop(p.atomic != 0, ticket);
+    main_loop(cur, p.atomic != 0, ticket);
     // The next item: the ticket taken during this tile, or the next stripe.
     if (p.atomic && tid == 0) *s_item = ticket;
     __syncthreads();  // every wave is done reading this tile's LDS stages; s_item is visible
@@ -644,18 +759,20 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
       if (s < nk) issue_stage(issued = s);
     cur = nxt;
     w = next;
+    scale_buf ^= 1;
   }
 }
 
-template <int BM, int BN, int SBK, int NSTAGE>
+template <int BM, int BN, int SBK, int NSTAGE, class T>
 constexpr int lds_bytes() {
-  return NSTAGE * (BM + BN) * SBK * 2;
+  return NSTAGE * (BM + BN) * SBK * T::kElem;
 }
 // Row offsets of the derived queue's experts are kept in LDS when they fit
 // beside the stages (otherwise each tile reads them from global memory).
-template <int BM, int BN, int SBK, int NSTAGE, int NT>
+template <int BM, int BN, int SBK, int NSTAGE, int NT, class T>
 constexpr bool offsets_in_lds() {
-  return lds_bytes<BM, BN, SBK, NSTAGE>() + 2 * 4 * (kMaxLdsExpertsGemm + 1) + 4 * NT + 256 <=
+  return lds_bytes<BM, BN, SBK, NSTAGE, T>() + 2 * 4 * (kMaxLdsExpertsGemm + 1) + 4 * NT + 256 +
+             (T::kScaled ? 8 * (BM + BN) : 0) <=
          160 * 1024;
 }
 
@@ -666,14 +783,15 @@ template <int BM, int BN, int SBK, int NSTAGE, int NW, class T, int EPI>
 __global__ __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64),
                           amdgpu_waves_per_eu(NW / 4, NW / 4))) void
 grouped_gemm_kernel(GemmParams p) {
-  static_assert(lds_bytes<BM, BN, SBK, NSTAGE>() <= 144 * 1024, "LDS stages exceed the budget");
+  static_assert(lds_bytes<BM, BN, SBK, NSTAGE, T>() <= 144 * 1024, "LDS stages exceed the budget");
   constexpr int NT = NW * 64;
-  constexpr bool kOffsLds = offsets_in_lds<BM, BN, SBK, NSTAGE, NT>();
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes<BM, BN, SBK, NSTAGE>()];
+  constexpr bool kOffsLds = offsets_in_lds<BM, BN, SBK, NSTAGE, NT, T>();
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes<BM, BN, SBK, NSTAGE, T>()];
   __shared__ int32_t s_prefix[kMaxLdsExpertsGemm + 1];
   __shared__ int32_t s_offs[kOffsLds ? kMaxLdsExpertsGemm + 1 : 1];
   __shared__ int32_t s_scan[NT];
   __shared__ int32_t s_item;
+  __shared__ float s_scale[T::kScaled ? 2 * (BM + BN) : 1];
 
   const int tid = threadIdx.x;
   const int G = gridDim.x;
@@ -705,7 +823,7 @@ grouped_gemm_kernel(GemmParams p) {
   }
   run_worker<BM, BN, SBK, NSTAGE, NW, T, EPI>(p, W, first, n_tiles, s_prefix,
                                          (kOffsLds && p.num_work < 0) ? s_offs : nullptr,
-                                         &s_item, lds);
+                                         &s_item, lds, s_scale);
   if (!p.atomic) return;
   // Every worker has fetched its final (out-of-range) ticket before adding to
   // `done`, so the last one to arrive reads the final count (W + G when no
@@ -752,6 +870,22 @@ int launch_typed(int block_m, int block_n, const GemmParams& p, int workers, hip
                                             : "fused epilogues need block_m == block_n in {128, 256}");
 }
 
+// fp8: 128-byte rows of K (K-wide 128 stages, two 64-deep MFMA steps).  Four
+// waves (one per SIMD): the 32-byte fp8 fragments double-buffered for eight
+// waves of a 256x256 tile do not fit beside its accumulators.
+int launch_fp8(int block_m, int block_n, const GemmParams& p, int workers, hipStream_t stream) {
+#define MGG_CASE(BM_, BN_, SBK_, NS_, NW_)                                                    \
+  if (block_m == BM_ && block_n == BN_) {                                                    \
+    hipLaunchKernelGGL((grouped_gemm_kernel<BM_, BN_, SBK_, NS_, NW_, Fp8, kEpiNone>),       \
+                       dim3(workers), dim3(NW_ * 64), 0, stream, p);                          \
+    return MGG_OK;                                                                            \
+  }
+  MGG_CASE(256, 128, 128, 3, 4)
+  MGG_CASE(128, 128, 128, 4, 4)
+#undef MGG_CASE
+  return set_error(MGG_ERR_UNSUPPORTED, "fp8 tiles are 256x128 and 128x128");
+}
+
 template <class T>
 int launch_epi(int epilogue, int block_m, int block_n, const GemmParams& p, int workers,
                hipStream_t stream) {
@@ -777,8 +911,10 @@ int launch_grouped_gemm(int dtype, int epilogue, int block_m, int block_n, const
     rc = launch_epi<Bf16>(epilogue, block_m, block_n, p, workers, stream);
   else if (dtype == MGG_DTYPE_FP16)
     rc = launch_epi<F16>(epilogue, block_m, block_n, p, workers, stream);
+  else if (dtype == MGG_DTYPE_FP8_E4M3 && epilogue == kEpiNone)
+    rc = launch_fp8(block_m, block_n, p, workers, stream);
   else
-    return set_error(MGG_ERR_UNSUPPORTED, "dtype must be MGG_DTYPE_BF16 or MGG_DTYPE_FP16");
+    return set_error(MGG_ERR_UNSUPPORTED, "unsupported dtype / epilogue combination");
   if (rc != MGG_OK) return rc;
   return hip_error(hipGetLastError(), "grouped_gemm_kernel launch");
 }

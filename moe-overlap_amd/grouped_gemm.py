@@ -46,6 +46,7 @@ __all__ = [
     "reference_grouped_gemm",
     "_build_work_queue",
     "grouped_gemm_flops",
+    "quantize_fp8_rows",
 ]
 
 _SUPPORTED_BLOCKS = (64, 128, 256)
@@ -221,6 +222,8 @@ def persistent_grouped_gemm(
     num_stages: int = 3,
     *,
     queue: str = "device",
+    a_scale: Optional[torch.Tensor] = None,
+    b_scale: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """C[s_e:t_e] = A[s_e:t_e] @ B[e] for every expert, persistent workers.
 
@@ -229,6 +232,13 @@ def persistent_grouped_gemm(
     [M, N] in the input dtype (rows outside every expert range are left
     uninitialised; an empty queue zero-fills).  Launches asynchronously on the
     current stream of a_cat's device.
+
+    Extension beyond the reference (which rejects fp8, :357-358): with
+    float8_e4m3fn a_cat and b_expert plus a_scale [M] (per token) and b_scale
+    [E, N] (per expert output channel), both fp32, the result is
+    a_scale[r] * b_scale[e, n] * (A @ B[e])[r, n] in bf16.  B is read K-major:
+    pass b_expert as a [E, K, N] view of [E, N, K] memory (stride(1) == 1,
+    e.g. w.transpose(1, 2) of a linear layer's [E, N, K] weight) to avoid a copy.
     """
     if a_cat.device.type != "cuda" or b_expert.device.type != "cuda":
         raise ValueError("persistent_grouped_gemm requires CUDA tensors.")
@@ -240,6 +250,10 @@ def persistent_grouped_gemm(
         raise ValueError("expert_offsets must have shape [num_experts + 1].")
     if expert_offsets.device != a_cat.device:
         raise ValueError("expert_offsets must be on the same device as input tensors.")
+    if a_cat.dtype == torch.float8_e4m3fn:
+        return _persistent_grouped_gemm_fp8(a_cat, b_expert, expert_offsets, a_scale, b_scale,
+                                            num_sms, block_m, block_n, use_atomic_queue,
+                                            work_counter)
     if a_cat.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("a_cat dtype must be bf16/fp16.")
     if b_expert.dtype != a_cat.dtype:
@@ -314,6 +328,83 @@ def persistent_grouped_gemm(
     if n_pad != n_size:
         return c_op[:, :n_size].contiguous()
     return c_op
+
+
+def _persistent_grouped_gemm_fp8(a_cat, b_expert, expert_offsets, a_scale, b_scale, num_sms,
+                                 block_m, block_n, use_atomic_queue, work_counter):
+    if b_expert.dtype != torch.float8_e4m3fn:
+        raise ValueError("b_expert dtype should match a_cat dtype.")
+    if a_scale is None or b_scale is None:
+        raise ValueError("fp8 operands need a_scale [M] and b_scale [E, N] (float32).")
+    m_total, k_size = a_cat.shape
+    num_experts, _, n_size = b_expert.shape
+    if a_scale.numel() != m_total or b_scale.numel() != num_experts * n_size:
+        raise ValueError("a_scale must have M entries and b_scale E*N entries.")
+    if a_scale.device != a_cat.device or b_scale.device != a_cat.device:
+        raise ValueError("scales must be on the same device as input tensors.")
+    device = a_cat.device
+    dev_index = device.index if device.index is not None else torch.cuda.current_device()
+    if block_m is None or block_n is None:
+        avg = m_total / max(num_experts, 1)
+        block_m = block_m or (256 if avg >= 256 else 128)
+        block_n = block_n or 128
+    if (block_m, block_n) not in ((256, 128), (128, 128)):
+        raise ValueError("fp8 tiles are block_m x block_n = 256x128 or 128x128.")
+    if num_sms is None:
+        num_sms = _cu_count(dev_index)
+    counter_dev = None
+    if use_atomic_queue and work_counter is not None:
+        if work_counter.numel() != 1 or work_counter.dtype != torch.int32:
+            raise ValueError("work_counter must be int32 tensor of shape [1].")
+        counter_dev = work_counter.to(device).contiguous()
+    # K to a multiple of 16, N to a multiple of 8 (zero padding adds nothing).
+    k_pad = (k_size + 15) // 16 * 16
+    n_pad = (n_size + 7) // 8 * 8
+    a_op = a_cat
+    if k_pad != k_size:
+        a_op = torch.nn.functional.pad(a_op.view(torch.uint8), (0, k_pad - k_size)).view(a_cat.dtype)
+    if a_op.stride(1) != 1 or a_op.stride(0) % 16 or a_op.data_ptr() % 16:
+        a_op = a_op.contiguous()
+    b_nk = b_expert.transpose(1, 2)  # [E, N, K]
+    if k_pad != k_size or n_pad != n_size:
+        b_nk = torch.nn.functional.pad(b_nk.contiguous().view(torch.uint8),
+                                       (0, k_pad - k_size, 0, n_pad - n_size)).view(b_expert.dtype)
+    if b_nk.stride(2) != 1 or b_nk.stride(1) % 16 or b_nk.stride(0) % 16 or b_nk.data_ptr() % 16:
+        b_nk = b_nk.contiguous()
+    sa = a_scale.reshape(-1).to(torch.float32).contiguous()
+    sb = b_scale.reshape(num_experts, n_size).to(torch.float32)
+    if n_pad != n_size:
+        sb = torch.nn.functional.pad(sb, (0, n_pad - n_size))
+    sb = sb.contiguous()
+    off32 = expert_offsets if expert_offsets.dtype == torch.int32 else expert_offsets.to(torch.int32)
+    off32 = off32.contiguous()
+    c_op = torch.empty((m_total, n_pad), device=device, dtype=torch.bfloat16)
+    lda = a_op.stride(0) if m_total > 1 else k_pad
+    ldb_n = b_nk.stride(1) if n_pad > 1 else k_pad
+    ldb_e = b_nk.stride(0) if num_experts > 1 else n_pad * ldb_n
+    args = (_ptr(a_op), _ptr(b_nk), _ptr(c_op), _ptr(off32), _ptr(sa), _ptr(sb),
+            m_total, k_pad, n_pad, num_experts, lda, ldb_e, ldb_n, c_op.stride(0),
+            int(block_m), int(block_n), int(num_sms), 1 if use_atomic_queue else 0,
+            _ptr(counter_dev), torch.cuda.current_stream(device).cuda_stream)
+    lib = _nat.lib()
+    if torch.cuda.current_device() == dev_index:
+        _nat.check(lib.mgg_grouped_gemm_fp8(*args))
+    else:
+        with torch.cuda.device(dev_index):
+            _nat.check(lib.mgg_grouped_gemm_fp8(*args))
+    if n_pad != n_size:
+        return c_op[:, :n_size].contiguous()
+    return c_op
+
+
+def quantize_fp8_rows(x: torch.Tensor, dim: int = -1):
+    """(x_fp8, scale) with scale = amax / 448 along `dim` (per row of x by
+    default), x_fp8 = float8_e4m3fn(x / scale): the per-token / per-channel
+    recipe of the fp8 config.  Input preparation (torch ops), not a kernel."""
+    amax = x.float().abs().amax(dim=dim, keepdim=True).clamp_min(1e-12)
+    scale = amax / 448.0
+    q = (x.float() / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q, scale.squeeze(dim)
 
 
 def reference_grouped_gemm(

@@ -22,6 +22,7 @@ MGG_ERR_HIP = 3
 
 MGG_DTYPE_BF16 = 0
 MGG_DTYPE_FP16 = 1
+MGG_DTYPE_FP8_E4M3 = 2
 MGG_INT32 = 0
 MGG_INT64 = 1
 MGG_EPI_NONE = 0
@@ -56,6 +57,13 @@ _SIGNATURES = {
         _c_i32, _c_i32, _c_ptr, _c_ptr, _c_ptr,  # dtype, epilogue, a, b, c
         _c_ptr, _c_i64, _c_i64, _c_i64,  # offsets, M, K, N
         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,  # E, lda, ldb_e, ldb_k, ldc
+        _c_i32, _c_i32, _c_i32, _c_i32,  # block_m, block_n, num_workers, atomic
+        _c_ptr, _c_ptr,  # work_counter, stream
+    ],
+    "mgg_grouped_gemm_fp8": [
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,  # a, b, c, offsets, a_scale, b_scale
+        _c_i64, _c_i64, _c_i64, _c_i64,  # M, K, N, E
+        _c_i64, _c_i64, _c_i64, _c_i64,  # lda, ldb_e, ldb_n, ldc
         _c_i32, _c_i32, _c_i32, _c_i32,  # block_m, block_n, num_workers, atomic
         _c_ptr, _c_ptr,  # work_counter, stream
     ],

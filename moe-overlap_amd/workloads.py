@@ -121,6 +121,66 @@ def make_expert_mlp_case(tokens: int = 8192, experts: int = 16, top_k: int = 2,
     return case
 
 
+@dataclass
+class Fp8Case:
+    """The BASELINE fp8 config: per-token scaled e4m3 activations, per-output-
+    channel scaled e4m3 expert weights stored [E, N, K] (K contiguous)."""
+
+    counts: torch.Tensor  # int32 [E] (CPU)
+    k: int
+    n: int
+    a: Optional[torch.Tensor] = None  # [M, K] float8_e4m3fn
+    a_scale: Optional[torch.Tensor] = None  # [M] fp32
+    b_nk: Optional[torch.Tensor] = None  # [E, N, K] float8_e4m3fn
+    b_scale: Optional[torch.Tensor] = None  # [E, N] fp32
+    a_ref: Optional[torch.Tensor] = None  # [M, K] fp32 before quantisation
+    b_ref: Optional[torch.Tensor] = None  # [E, N, K] fp32 before quantisation
+
+    @property
+    def num_experts(self) -> int:
+        return int(self.counts.numel())
+
+    @property
+    def m(self) -> int:
+        return int(self.counts.sum())
+
+    @property
+    def flops(self) -> int:
+        return 2 * self.m * self.k * self.n
+
+    def algorithmic_bytes(self) -> int:
+        """fp8 A and the non-empty experts' fp8 B read once, bf16 C written
+        once, plus the fp32 scales (4M + 4 E_nonempty N)."""
+        nonempty = int((self.counts > 0).sum())
+        return (self.m * self.k + nonempty * self.k * self.n + 2 * self.m * self.n
+                + 4 * self.m + 4 * nonempty * self.n)
+
+
+def make_fp8_case(tokens: int = 4096, experts: int = 64, top_k: int = 6, k: int = 2048,
+                  n: int = 1408, device=None, seed: int = 0, keep_reference: bool = False) -> Fp8Case:
+    """Synthetic inputs of the fp8 config (defaults: BASELINE cfg 5): counts of
+    top-k routing on N(0,1) logits, X ~ N(0,1), W ~ N(0, 1/K), each quantised
+    with scale = amax / 448 per token and per output channel."""
+    counts = topk_counts(tokens, experts, top_k)
+    case = Fp8Case(counts, k, n)
+    device = torch.device("cpu") if device is None else torch.device(device)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    x = torch.randn(case.m, k, generator=gen, device=device, dtype=torch.float32)
+    w = torch.randn(experts, n, k, generator=gen, device=device, dtype=torch.float32)
+    w.mul_(1.0 / math.sqrt(k))
+
+    def quant(t):
+        amax = t.abs().amax(dim=-1, keepdim=True).clamp_min(1e-12)
+        scale = amax / 448.0
+        return (t / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn), scale.squeeze(-1)
+
+    case.a, case.a_scale = quant(x)
+    case.b_nk, case.b_scale = quant(w)
+    if keep_reference:
+        case.a_ref, case.b_ref = x, w
+    return case
+
+
 def make_case(
     name: str,
     device: Optional[torch.device] = None,

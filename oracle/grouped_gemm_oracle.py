@@ -21,6 +21,13 @@ Functions and what pins each one (tests/test_oracle_*.py):
   experts), expert-scaled identities, E=1 reducing to a plain matmul, and
   integer-valued inputs with exact expected outputs.
 * ``queue_coverage`` -- the coverage invariant itself (a counting check).
+* ``fp8_e4m3_to_f32`` / ``grouped_gemm_fp8`` -- the fp8 extension (the
+  reference rejects fp8 at :357-358): OCP e4m3 decoded from its definition
+  (sign, 4-bit exponent with bias 7, 3-bit mantissa, subnormals, 0x7F/0xFF
+  NaN, no infinities), then the per-expert product scaled per row of A and
+  per (expert, column).  Pinned by torch's own float8_e4m3fn conversion on
+  all 256 codes, by closed-form codes (1.0, 448, the smallest subnormal), and
+  by reduction to ``grouped_gemm`` on the decoded values.
 """
 from __future__ import annotations
 
@@ -34,6 +41,8 @@ __all__ = [
     "queue_coverage",
     "bf16_bits_to_f32",
     "f32_to_bf16_bits",
+    "fp8_e4m3_to_f32",
+    "grouped_gemm_fp8",
 ]
 
 
@@ -145,3 +154,36 @@ def f32_to_bf16_bits(x) -> np.ndarray:
     out = rounded.astype(np.uint16)
     out[np.isnan(x.reshape(-1))] = 0x7FC0
     return out.reshape(x.shape)
+
+
+def fp8_e4m3_to_f32(bits) -> np.ndarray:
+    """OCP e4m3 (float8_e4m3fn) bytes -> float32: (-1)^s * 2^(e-7) * (1 + m/8),
+    subnormals 2^-6 * m/8 for e == 0, NaN for exponent and mantissa all ones."""
+    b = np.asarray(bits, dtype=np.uint8).astype(np.int64)
+    sign = np.where(b & 0x80, -1.0, 1.0)
+    e = (b >> 3) & 0xF
+    m = b & 0x7
+    val = np.where(e == 0, np.ldexp(m / 8.0, -6), np.ldexp(1.0 + m / 8.0, e - 7))
+    val = np.where((e == 0xF) & (m == 0x7), np.nan, val)
+    return (sign * val).astype(np.float32)
+
+
+def grouped_gemm_fp8(a_bits, b_bits_nk, offsets, a_scale, b_scale, acc_dtype=np.float64,
+                     magnitude: bool = False) -> np.ndarray:
+    """C[r, n] = a_scale[r] * b_scale[e, n] * sum_k A[r, k] * B[e, n, k] over
+    each expert's row range (rows outside every range are zero here).
+    a_bits [M, K] and b_bits_nk [E, N, K] are e4m3 bytes.  With magnitude=True
+    the same with |A| and |B| (the scale of the sum's rounding errors)."""
+    a = fp8_e4m3_to_f32(a_bits).astype(acc_dtype)
+    b = fp8_e4m3_to_f32(b_bits_nk).astype(acc_dtype)
+    if magnitude:
+        a, b = np.abs(a), np.abs(b)
+    offs = np.asarray(offsets, dtype=np.int64)
+    sa = np.asarray(a_scale, dtype=acc_dtype).reshape(-1)
+    sb = np.asarray(b_scale, dtype=acc_dtype).reshape(b.shape[0], b.shape[1])
+    out = np.zeros((a.shape[0], b.shape[1]), dtype=acc_dtype)
+    for e in range(b.shape[0]):
+        s, t = int(offs[e]), int(offs[e + 1])
+        if t > s:
+            out[s:t] = (a[s:t] @ b[e].T) * sa[s:t, None] * sb[e][None, :]
+    return out

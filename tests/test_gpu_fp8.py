@@ -1,0 +1,124 @@
+"""GPU parity of the fp8 (OCP e4m3) grouped GEMM with per-token and
+per-output-channel scales, through libmgg's C ABI (mgg_grouped_gemm_fp8,
+reached via persistent_grouped_gemm's fp8 extension).
+
+Reference: the oracle's decoded-fp8 product in float64
+(oracle.grouped_gemm_oracle.grouped_gemm_fp8).  The kernel multiplies the
+exact fp8 values, accumulates in fp32 and rounds once to bf16, so against the
+decoded reference |C - ref| <= 2^-8 |ref| + 2^-16 * mag, where mag =
+a_scale * b_scale * sum_k |a_k| |b_k| bounds the accumulation's rounding
+(outputs near zero come from partial sums ~1e4 times larger).  Against the
+unquantised fp32 GEMM the BASELINE north_star bound applies: relative
+(Frobenius) error <= 5e-2.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import grouped_gemm as gg
+import workloads
+from oracle import grouped_gemm_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def fp8_inputs(counts, k, n, seed=0, device="cpu"):
+    gen = torch.Generator().manual_seed(seed)
+    m = int(sum(counts))
+    x = torch.randn(m, k, generator=gen)
+    w = torch.randn(len(counts), n, k, generator=gen) / math.sqrt(k)
+    a, sa = gg.quantize_fp8_rows(x)
+    b, sb = gg.quantize_fp8_rows(w)
+    offs = torch.tensor(orc.expert_offsets_from_recv_counts(counts), dtype=torch.int32)
+    return [t.to(device) for t in (a, sa, b, sb, offs)]
+
+
+def oracle_fp8(a, sa, b_nk, sb, offs, magnitude=False):
+    return orc.grouped_gemm_fp8(a.cpu().view(torch.uint8).numpy(), b_nk.cpu().view(torch.uint8).numpy(),
+                                offs.cpu().numpy(), sa.cpu().numpy(), sb.cpu().numpy(),
+                                magnitude=magnitude)
+
+
+def assert_close_fp8(c, a, sa, b, sb, offs):
+    rows = a.shape[0]
+    ref = oracle_fp8(a, sa, b, sb, offs)[:rows]
+    mag = oracle_fp8(a, sa, b, sb, offs, magnitude=True)[:rows]
+    c = c.float().cpu().numpy()[:rows]
+    bound = 2 ** -8 * np.abs(ref) + 2 ** -16 * mag
+    err = np.abs(c - ref)
+    assert np.all(err <= bound), float((err - bound).max())
+
+
+@pytest.mark.parametrize("block_m,block_n", [(256, 128), (128, 128)])
+@pytest.mark.parametrize("atomic", [False, True])
+def test_fp8_small_ragged(cuda_device, block_m, block_n, atomic):
+    log(f"fp8 small {block_m}x{block_n} atomic={atomic}")
+    counts = [37, 0, 300, 5, 129]
+    a, sa, b, sb, offs = fp8_inputs(counts, 512, 320, device=cuda_device)
+    c = gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, block_m=block_m, block_n=block_n,
+                                   use_atomic_queue=atomic, a_scale=sa, b_scale=sb)
+    assert c.dtype == torch.bfloat16 and tuple(c.shape) == (a.shape[0], 320)
+    assert_close_fp8(c, a, sa, b, sb, offs)
+
+
+def test_fp8_padded_shapes_and_b_layouts(cuda_device):
+    log("fp8 padded")
+    counts = [9, 70, 0, 33]
+    a, sa, b, sb, offs = fp8_inputs(counts, 40, 20, seed=3, device=cuda_device)
+    c_view = gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, a_scale=sa, b_scale=sb)
+    c_copy = gg.persistent_grouped_gemm(a, b.transpose(1, 2).contiguous(), offs, a_scale=sa,
+                                        b_scale=sb)
+    assert torch.equal(c_view, c_copy)
+    assert_close_fp8(c_view, a, sa, b, sb, offs)
+
+
+def test_fp8_work_counter_and_errors(cuda_device):
+    counts = [300, 300]
+    a, sa, b, sb, offs = fp8_inputs(counts, 256, 256, device=cuda_device)
+    wc = torch.zeros(1, dtype=torch.int32, device=cuda_device)
+    gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, num_sms=7, block_m=128, block_n=128,
+                               work_counter=wc, a_scale=sa, b_scale=sb)
+    torch.cuda.synchronize()
+    assert int(wc.item()) == 2 * 3 * 2 + 7  # W = sum ceil(300/128) * ceil(256/128)
+    with pytest.raises(ValueError, match="a_scale"):
+        gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs)
+    with pytest.raises(ValueError, match="256x128 or 128x128"):
+        gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, block_m=64, block_n=64,
+                                   a_scale=sa, b_scale=sb)
+
+
+def test_fp8_baseline_config(cuda_device):
+    """BASELINE fp8 config: E=64, M=24576 (top-6 of 4096 tokens), K=2048,
+    N=1408; against the decoded-fp8 fp32 product per expert on the GPU and
+    against the unquantised fp32 GEMM (north_star: relative error <= 5e-2)."""
+    log("fp8 cfg5")
+    case = workloads.make_fp8_case(device=cuda_device, keep_reference=True)
+    offs = gg.expert_offsets_from_recv_counts(case.counts, device=cuda_device)
+    c = gg.persistent_grouped_gemm(case.a, case.b_nk.transpose(1, 2), offs,
+                                   a_scale=case.a_scale, b_scale=case.b_scale).float()
+    o = offs.cpu().tolist()
+    num = den = unq_num = 0.0
+    worst = 0.0
+    for e in range(case.num_experts):
+        s, t = o[e], o[e + 1]
+        if t <= s:
+            continue
+        sa_e, sb_e = case.a_scale[s:t, None], case.b_scale[e][:, None]
+        deq = (case.a[s:t].float() * sa_e) @ (case.b_nk[e].float() * sb_e).t()
+        mag = (case.a[s:t].float().abs() * sa_e) @ (case.b_nk[e].float().abs() * sb_e).t()
+        bound = 2 ** -8 * deq.abs() + 2 ** -16 * mag
+        worst = max(worst, ((c[s:t] - deq).abs() - bound).max().item())
+        exact = case.a_ref[s:t] @ case.b_ref[e].t()
+        unq_num += (c[s:t] - exact).pow(2).sum().item()
+        den += exact.pow(2).sum().item()
+    rel = math.sqrt(unq_num / den)
+    log(f"cfg5: worst excess over the decoded bound {worst:.3g}, rel error vs unquantised {rel:.4f}")
+    assert worst <= 0.0
+    assert rel <= 5e-2

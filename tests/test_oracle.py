@@ -217,3 +217,42 @@ def test_bf16_matches_torch_rounding():
     x = np.random.default_rng(4).standard_normal(10_000).astype(np.float32) * 100
     want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     np.testing.assert_array_equal(orc.f32_to_bf16_bits(x), want)
+
+
+def test_fp8_decode_matches_torch_on_every_code():
+    import torch
+
+    codes = np.arange(256, dtype=np.uint8)
+    ours = orc.fp8_e4m3_to_f32(codes)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert nan.sum() == 2  # 0x7F and 0xFF
+    np.testing.assert_array_equal(ours[~nan], ref[~nan])
+
+
+def test_fp8_decode_closed_forms():
+    assert orc.fp8_e4m3_to_f32([0x38])[0] == 1.0
+    assert orc.fp8_e4m3_to_f32([0x7E])[0] == 448.0  # largest finite
+    assert orc.fp8_e4m3_to_f32([0x01])[0] == 2.0 ** -9  # smallest subnormal
+    assert orc.fp8_e4m3_to_f32([0xC0])[0] == -2.0
+    assert orc.fp8_e4m3_to_f32([0x80])[0] == 0.0 and np.signbit(orc.fp8_e4m3_to_f32([0x80])[0])
+
+
+def test_fp8_grouped_gemm_reduces_to_dequantized_grouped_gemm():
+    rng = np.random.default_rng(11)
+    counts = [3, 0, 5, 2]
+    offs = orc.expert_offsets_from_recv_counts(counts)
+    M, K, N, E = int(offs[-1]) + 1, 32, 6, len(counts)
+    a = rng.integers(0, 256, size=(M, K), dtype=np.uint8)
+    b = rng.integers(0, 256, size=(E, N, K), dtype=np.uint8)
+    a[(a & 0x7F) == 0x7F] = 0x38  # no NaN codes
+    b[(b & 0x7F) == 0x7F] = 0x38
+    sa = rng.random(M) + 0.5
+    sb = rng.random((E, N)) + 0.5
+    got = orc.grouped_gemm_fp8(a, b, offs, sa, sb)
+    deq_b = np.transpose(orc.fp8_e4m3_to_f32(b).astype(np.float64), (0, 2, 1)) * sb[:, None, :]
+    deq_a = orc.fp8_e4m3_to_f32(a).astype(np.float64) * sa[:, None]
+    ref = orc.grouped_gemm(deq_a, deq_b, offs, acc_dtype=np.float64)
+    rows = int(offs[-1])
+    np.testing.assert_allclose(got[:rows], ref[:rows], rtol=1e-12, atol=1e-9)
