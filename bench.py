@@ -32,6 +32,7 @@ sys.path.insert(0, str(REPO))
 METRIC = "grouped GEMM TFLOP/s + % bf16 MFMA peak, E=16 512 tok/expert K2048 N4096"
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0
+PEAK_FP8_TFLOPS = 5033.2  # MI355X dense fp8 MFMA
 KERNEL_NAME = "grouped_gemm_kernel<256,256,64,2,8,Bf16,0>"
 
 
@@ -139,6 +140,42 @@ def expert_mlp_summary(dev, steps: int = 10):
     out["down_gemm_tflops"] = round(down_flops / (lm["down_gemm"] * 1e-3) / 1e12, 1)
     del case, w1, lay, xp, h, y
     torch.cuda.empty_cache()
+    return out
+
+
+def fp8_summary(dev, steps: int = 20):
+    """The BASELINE fp8 config (E=64, M=24576, K=2048, N=1408, e4m3 with
+    per-token x per-channel scales, bf16 out), HBM-bound by its algorithmic
+    bytes: each tile shape and schedule, kernel time from HIP events."""
+    import grouped_gemm as gg
+    import workloads
+
+    case = workloads.make_fp8_case(device=dev)
+    offs = gg.expert_offsets_from_recv_counts(case.counts, device=dev)
+    b_kn = case.b_nk.transpose(1, 2)
+    t_bytes = case.algorithmic_bytes()
+    t_flop_bound = case.flops / (PEAK_FP8_TFLOPS * 1e12)
+    t_hbm_bound = t_bytes / (PEAK_HBM_GBPS * 1e9)
+    out = {"config": f"E={case.num_experts}, M={case.m}, K={case.k}, N={case.n}, e4m3 in, bf16 out",
+           "algorithmic_bytes": t_bytes, "t_bound_us": round(max(t_flop_bound, t_hbm_bound) * 1e6, 2),
+           "runs": {}}
+    best = None
+    for bm, bn in ((256, 128), (128, 128)):
+        for mode in ("striped", "atomic"):
+            fn = lambda: gg.persistent_grouped_gemm(case.a, b_kn, offs, block_m=bm, block_n=bn,
+                                                    use_atomic_queue=mode == "atomic",
+                                                    a_scale=case.a_scale, b_scale=case.b_scale)
+            event_times_ms(fn, 3)
+            t = median(event_times_ms(fn, steps))
+            r = {"kernel_ms_median": round(t, 4),
+                 "tflops": round(case.flops / (t * 1e-3) / 1e12, 1),
+                 "hbm_gbps_at_algorithmic_bytes": round(t_bytes / (t * 1e-3) / 1e9, 1)}
+            out["runs"][f"{bm}x{bn}_{mode}"] = r
+            if best is None or t < best[1]:
+                best = (f"{bm}x{bn}_{mode}", t)
+    out["best"] = best[0]
+    out["best_frac_of_hbm_roofline"] = round(t_hbm_bound * 1e3 / best[1], 4)
+    out["best_pct_fp8_peak"] = round(100 * case.flops / (best[1] * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 2)
     return out
 
 
@@ -272,6 +309,7 @@ def main():
         extra["torch_loop_gpu_ms_median"] = round(median(tl), 4)
         extra["torch_loop_gpu_tflops"] = round(flops / (median(tl) * 1e-3) / 1e12, 1)
         extra["expert_mlp"] = expert_mlp_summary(dev)
+        extra["fp8"] = fp8_summary(dev)
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(case, args.cpu_seconds)
 

@@ -25,6 +25,9 @@
 #ifndef MGG_NW256
 #define MGG_NW256 8
 #endif
+#ifndef MGG_FP8_NW
+#define MGG_FP8_NW 8
+#endif
 
 namespace mgg {
 namespace {
@@ -870,9 +873,10 @@ int launch_typed(int block_m, int block_n, const GemmParams& p, int workers, hip
                                             : "fused epilogues need block_m == block_n in {128, 256}");
 }
 
-// fp8: 128-byte rows of K (K-wide 128 stages, two 64-deep MFMA steps).  Four
-// waves (one per SIMD): the 32-byte fp8 fragments double-buffered for eight
-// waves of a 256x256 tile do not fit beside its accumulators.
+// fp8: 128-byte rows of K (K-wide 128 stages, two 64-deep MFMA steps), eight
+// waves (two per SIMD) on 256x128 and 128x128 tiles.  A 256x256 tile does not
+// fit: its 32-byte fp8 fragments, double-buffered, and its accumulators need
+// more than the 256 registers a wave has at two waves per SIMD.
 int launch_fp8(int block_m, int block_n, const GemmParams& p, int workers, hipStream_t stream) {
 #define MGG_CASE(BM_, BN_, SBK_, NS_, NW_)                                                    \
   if (block_m == BM_ && block_n == BN_) {                                                    \
@@ -880,8 +884,8 @@ int launch_fp8(int block_m, int block_n, const GemmParams& p, int workers, hipSt
                        dim3(workers), dim3(NW_ * 64), 0, stream, p);                          \
     return MGG_OK;                                                                            \
   }
-  MGG_CASE(256, 128, 128, 3, 4)
-  MGG_CASE(128, 128, 128, 4, 4)
+  MGG_CASE(256, 128, 128, 3, MGG_FP8_NW)
+  MGG_CASE(128, 128, 128, 4, MGG_FP8_NW)
 #undef MGG_CASE
   return set_error(MGG_ERR_UNSUPPORTED, "fp8 tiles are 256x128 and 128x128");
 }
