@@ -41,7 +41,10 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--workload", default="uniform", choices=["uniform", "skewed", "cpu_plumbing"])
+    p.add_argument("--workload", default="uniform",
+                   choices=["uniform", "skewed", "cpu_plumbing", "expert_mlp", "fp8"],
+                   help="uniform (the metric's config), skewed, cpu_plumbing; expert_mlp and fp8 "
+                        "time the BASELINE expert-MLP forward / fp8 GEMM configs instead")
     p.add_argument("--mode", default="atomic", choices=["atomic", "striped"])
     p.add_argument("--block-m", type=int, default=256)
     p.add_argument("--block-n", type=int, default=256)
@@ -78,13 +81,21 @@ def event_times_ms(fn, iters, flush=None):
 PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_256x256_bf16_uniform.md"
 
 
+FP8_PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_fp8_256x128_cfg5.md"
+
+
 def recorded_traffic(mode, workload, block_m, block_n):
-    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
-    (calibrated against a plain copy), when it covers this configuration; else None."""
-    if workload != "uniform" or (block_m, block_n) != (256, 256) or not PROFILE_SUMMARY.exists():
+    """HBM bytes per launch from a committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+    (calibrated against a plain copy), when one covers this configuration; else None."""
+    if workload == "uniform" and (block_m, block_n) == (256, 256):
+        path, key = PROFILE_SUMMARY, f"traffic_bytes_per_launch_{mode}:"
+    elif workload == "fp8" and (block_m, block_n) == (256, 128):
+        path, key = FP8_PROFILE_SUMMARY, f"traffic_bytes_per_launch_fp8_{mode}:"
+    else:
         return None
-    key = f"traffic_bytes_per_launch_{mode}:"
-    for line in PROFILE_SUMMARY.read_text().splitlines():
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
         if line.startswith(key):
             return int(line.split(":", 1)[1])
     return None
@@ -216,6 +227,76 @@ def cpu_baseline(case, budget_s):
     }
 
 
+def secondary_main(args, dev):
+    """--workload expert_mlp | fp8: time one step of that config (the same
+    warmup / timed-steps / event protocol as the headline) and print its line."""
+    import torch
+
+    import expert_mlp as mlp
+    import grouped_gemm as gg
+    import workloads
+
+    if args.workload == "expert_mlp":
+        case = workloads.make_expert_mlp_case(device=dev)
+        w1 = mlp.interleave_gate_up(case.w_gate, case.w_up)
+        case.w_gate = case.w_up = None
+        step = lambda: mlp.expert_mlp_forward(case.x, case.topk_idx, case.topk_weight, w1, case.w2,
+                                              "swiglu", num_sms=args.num_sms,
+                                              use_atomic_queue=args.mode == "atomic")
+        flops, nbytes, bound, peak, dtype = case.flops, None, "mfma", PEAK_BF16_TFLOPS, "bf16"
+        metric = "expert-MLP forward TFLOP/s (SwiGLU, T=8192 top-2 of 16, H2048 F4096)"
+        config_blocks = (256, 256)
+        config = {"workload": f"expert_mlp: T={case.tokens}, top-{case.top_k} of E={case.experts}, "
+                              f"H={case.hidden}, F={case.ffn}, SwiGLU", "mode": args.mode}
+    else:
+        case = workloads.make_fp8_case(device=dev)
+        offs = gg.expert_offsets_from_recv_counts(case.counts, device=dev)
+        b_kn = case.b_nk.transpose(1, 2)
+        bm, bn = (256, 128) if (args.block_m, args.block_n) == (256, 256) else (args.block_m, args.block_n)
+        step = lambda: gg.persistent_grouped_gemm(case.a, b_kn, offs, num_sms=args.num_sms,
+                                                  block_m=bm, block_n=bn,
+                                                  use_atomic_queue=args.mode == "atomic",
+                                                  a_scale=case.a_scale, b_scale=case.b_scale)
+        flops, nbytes, bound, peak, dtype = case.flops, case.algorithmic_bytes(), "hbm", PEAK_HBM_GBPS, "fp8_e4m3"
+        metric = "fp8 grouped GEMM TFLOP/s, E=64 M=24576 K2048 N1408 (per-token x per-channel scales)"
+        config = {"workload": f"fp8: E={case.num_experts}, M={case.m}, K={case.k}, N={case.n}",
+                  "mode": args.mode, "block_m": bm, "block_n": bn}
+        config_blocks = (bm, bn)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record()
+        step()
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    if args.profile_only:
+        print(json.dumps({"profile_only": True, "workload": args.workload,
+                          "ms_per_step": wall / args.steps * 1e3}))
+        return
+    k_mean = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / args.steps
+    value = flops * args.steps / wall / 1e12
+    if bound == "hbm":
+        achieved, unit = nbytes / (k_mean * 1e-3) / 1e9, "GB/s"
+    else:
+        achieved, unit = flops / (k_mean * 1e-3) / 1e12, "TFLOP/s"
+    print(json.dumps({
+        "metric": metric, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+        "data": "synthetic (BASELINE recipe, random init)", "config": config,
+        "kernel_ms_mean": round(k_mean, 5),
+        "roofline": {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+                     "frac": round(achieved / peak, 4),
+                     "traffic": recorded_traffic(args.mode, args.workload, *config_blocks),
+                     "algorithmic_flops_per_step": flops, "algorithmic_bytes_per_step": nbytes},
+    }), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -238,6 +319,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": n * 4, "copies": args.warmup + args.steps}))
+        return
+    if args.workload in ("expert_mlp", "fp8"):
+        secondary_main(args, dev)
         return
     case = workloads.make_case(args.workload, device=dev, dtype=torch.bfloat16)
     offs = gg.expert_offsets_from_recv_counts(case.counts, device=dev)
