@@ -663,6 +663,23 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   // blocks are gate and up of the same 32 outputs and C has N/2 columns.
   static_assert(EPI != kEpiSwiglu || kNB == 2, "SwiGLU needs two 32-column blocks per wave");
   static_assert(EPI == kEpiNone || !T::kScaled, "fused epilogues are for unscaled types");
+  // Stores: a lane holds 4 consecutive columns of each 8-column group g; the
+  // lanes l and l+32 of one row swap halves of groups (2p, 2p+1) with
+  // v_permlane32_swap so that each lane stores 8 consecutive columns (16 bytes)
+  // and a row segment of 32 contiguous bytes goes out per pair of lanes.
+  auto store_pair = [&](uint16_t* crow, int64_t col, int64_t cols, bool row_ok,
+                        const float* y0, const float* y1) {
+    // y0: this lane's 4 values of group 2p, y1: of group 2p+1
+    const uint32_t a0 = T::pack(y0[0], y0[1]), a1 = T::pack(y0[2], y0[3]);
+    const uint32_t b0 = T::pack(y1[0], y1[1]), b1 = T::pack(y1[2], y1[3]);
+    const auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
+    const auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
+    // lanes 0-31: columns col..col+7; lanes 32-63: col+8..col+15 (col already includes 8*half)
+    if (row_ok && col < cols) {
+      const u32x4 v = {(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
+      *reinterpret_cast<u32x4*>(crow + col) = v;
+    }
+  };
   auto epilogue = [&](const Coords& c) {
     const float* sc = s_scale + scale_buf * (BM + BN);
 #pragma unroll
@@ -675,38 +692,32 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
       if constexpr (EPI == kEpiSwiglu) {
         const int64_t f0 = (c.n0 + wn * (BN / kWN)) / 2;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int64_t f = f0 + 8 * g + 4 * half;
-          if (row_ok && f < p.n / 2) {
-            float y[4];
+        for (int pp = 0; pp < 2; ++pp) {
+          float y0[4], y1[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) y[q] = silu_mul(acc[0][j][4 * g + q], acc[1][j][4 * g + q]);
-            u32x2 v;
-            v[0] = T::pack(y[0], y[1]);
-            v[1] = T::pack(y[2], y[3]);
-            *reinterpret_cast<u32x2*>(crow + f) = v;
+          for (int q = 0; q < 4; ++q) {
+            y0[q] = silu_mul(acc[0][j][8 * pp + q], acc[1][j][8 * pp + q]);
+            y1[q] = silu_mul(acc[0][j][8 * pp + 4 + q], acc[1][j][8 * pp + 4 + q]);
           }
+          store_pair(crow, f0 + 16 * pp + 8 * half, p.n / 2, row_ok, y0, y1);
         }
       } else {
 #pragma unroll
         for (int i = 0; i < kNB; ++i) {
+          const int cb = wn * (BN / kWN) + 32 * i;  // tile column of the block
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int64_t n = c.n0 + wn * (BN / kWN) + 32 * i + 8 * g + 4 * half;
-            if (row_ok && n < p.n) {
-              float y[4];
+          for (int pp = 0; pp < 2; ++pp) {
+            float y[2][4];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
               for (int q = 0; q < 4; ++q) {
+                const int g = 2 * pp + h;
                 float v = acc[i][j][4 * g + q];
-                if constexpr (T::kScaled)
-                  v *= row_scale * sc[BM + wn * (BN / kWN) + 32 * i + 8 * g + 4 * half + q];
-                y[q] = EPI == kEpiGelu ? gelu_erf(v) : v;
+                if constexpr (T::kScaled) v *= row_scale * sc[BM + cb + 8 * g + 4 * half + q];
+                y[h][q] = EPI == kEpiGelu ? gelu_erf(v) : v;
               }
-              u32x2 v;
-              v[0] = T::pack(y[0], y[1]);
-              v[1] = T::pack(y[2], y[3]);
-              *reinterpret_cast<u32x2*>(crow + n) = v;
-            }
+            store_pair(crow, c.n0 + cb + 16 * pp + 8 * half, p.n, row_ok, y[0], y[1]);
           }
         }
       }
