@@ -190,6 +190,56 @@ def fp8_summary(dev, steps: int = 20):
     return out
 
 
+def overlap_summary(case, offs, dev, steps: int = 10):
+    """What one GPU shows of the multi-GPU overlap design: (1) the GEMM with
+    CUs held back for communication kernels (num_sms < 256, the analogue of
+    the reference's DeepEP SM reservation), (2) the GEMM on one stream while a
+    copy of the next micro-batch's tokens runs on another stream (the local
+    memory traffic of a dispatch), against the two back to back."""
+    import torch
+
+    import grouped_gemm as gg
+
+    out = {"cu_reservation_ms": {}}
+    for sms in (256, 240, 224, 192):
+        fn = lambda: gg.persistent_grouped_gemm(case.a, case.b, offs, num_sms=sms)
+        event_times_ms(fn, 2)
+        out["cu_reservation_ms"][str(sms)] = round(median(event_times_ms(fn, steps)), 4)
+    # dispatch-sized copy: the tokens of a micro-batch (M x K bf16, 32 MiB), moved twice
+    # (send and receive buffers of an all-to-all on one rank)
+    src = torch.empty_like(case.a)
+    dst = torch.empty_like(case.a)
+    side = torch.cuda.Stream(device=dev)
+    main = torch.cuda.current_stream(dev)
+
+    def copies():
+        dst.copy_(src)
+        src.copy_(dst)
+
+    def serial():
+        gg.persistent_grouped_gemm(case.a, case.b, offs, num_sms=224)
+        copies()
+
+    def overlapped(sms):
+        # the GEMM is submitted first so that its workgroups take their CUs before the
+        # copy's many small workgroups fill the rest
+        side.wait_stream(main)
+        gg.persistent_grouped_gemm(case.a, case.b, offs, num_sms=sms)
+        with torch.cuda.stream(side):
+            copies()
+        main.wait_stream(side)
+
+    for name, fn in (("serial_ms", serial), ("overlapped_ms", lambda: overlapped(224)),
+                     ("overlapped_all_cus_ms", lambda: overlapped(256))):
+        event_times_ms(fn, 2)
+        out[name] = round(median(event_times_ms(fn, steps)), 4)
+    event_times_ms(copies, 2)
+    out["copy_alone_ms"] = round(median(event_times_ms(copies, steps)), 4)
+    out["note"] = ("GEMM at num_sms=224 (32 CUs left for the copy), copy = 2 x 32 MiB device "
+                   "copies on a second stream of default priority")
+    return out
+
+
 def cpu_baseline(case, budget_s):
     """The oracle's per-expert fp32 loop on the host cores, on a sample of experts."""
     import numpy as np
@@ -392,6 +442,7 @@ def main():
         tl = event_times_ms(loop, 5)
         extra["torch_loop_gpu_ms_median"] = round(median(tl), 4)
         extra["torch_loop_gpu_tflops"] = round(flops / (median(tl) * 1e-3) / 1e12, 1)
+        extra["overlap"] = overlap_summary(case, offs, dev)
         extra["expert_mlp"] = expert_mlp_summary(dev)
         extra["fp8"] = fp8_summary(dev)
 

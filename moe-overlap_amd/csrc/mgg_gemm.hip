@@ -659,9 +659,9 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   // ---- epilogue: acc[i][j] register r holds D[n][m] of the 32x32 block with
   // n = 8*(r/4) + 4*(lane/32) + r%4, m = lane%32 (D = C^T).  With the SwiGLU
   // epilogue B's columns come interleaved in groups of 64 (32 gate columns,
-  // then the 32 up columns of the same outputs), so a wave's two 32-column
-  // blocks are gate and up of the same 32 outputs and C has N/2 columns.
-  static_assert(EPI != kEpiSwiglu || kNB == 2, "SwiGLU needs two 32-column blocks per wave");
+  // then the 32 up columns of the same outputs), so a wave's 32-column blocks
+  // 2i and 2i+1 are gate and up of the same 32 outputs and C has N/2 columns.
+  static_assert(EPI != kEpiSwiglu || kNB % 2 == 0, "SwiGLU needs pairs of 32-column blocks per wave");
   static_assert(EPI == kEpiNone || !T::kScaled, "fused epilogues are for unscaled types");
   // Stores: a lane holds 4 consecutive columns of each 8-column group g; the
   // lanes l and l+32 of one row swap halves of groups (2p, 2p+1) with
@@ -690,16 +690,19 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
       const bool row_ok = m < c.rows_valid && grow >= 0 && grow <= last_row;
       uint16_t* crow = p.c + grow * p.ldc;
       if constexpr (EPI == kEpiSwiglu) {
-        const int64_t f0 = (c.n0 + wn * (BN / kWN)) / 2;
 #pragma unroll
-        for (int pp = 0; pp < 2; ++pp) {
-          float y0[4], y1[4];
+        for (int ip = 0; ip < kNB / 2; ++ip) {
+          const int64_t f0 = (c.n0 + wn * (BN / kWN) + 64 * ip) / 2;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            y0[q] = silu_mul(acc[0][j][8 * pp + q], acc[1][j][8 * pp + q]);
-            y1[q] = silu_mul(acc[0][j][8 * pp + 4 + q], acc[1][j][8 * pp + 4 + q]);
+          for (int pp = 0; pp < 2; ++pp) {
+            float y0[4], y1[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              y0[q] = silu_mul(acc[2 * ip][j][8 * pp + q], acc[2 * ip + 1][j][8 * pp + q]);
+              y1[q] = silu_mul(acc[2 * ip][j][8 * pp + 4 + q], acc[2 * ip + 1][j][8 * pp + 4 + q]);
+            }
+            store_pair(crow, f0 + 16 * pp + 8 * half, p.n / 2, row_ok, y0, y1);
           }
-          store_pair(crow, f0 + 16 * pp + 8 * half, p.n / 2, row_ok, y0, y1);
         }
       } else {
 #pragma unroll
