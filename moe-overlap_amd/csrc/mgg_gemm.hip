@@ -348,14 +348,14 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   };
 
   // ---- DMA sources ---------------------------------------------------------
-  // Each descriptor ends exactly at the last element of its operand, so a
-  // DMA past it writes zeros: rows of A past M, rows of B past K.  Rows of A
-  // inside [0, M) but past this expert's count bring the next expert's data;
-  // their results are never stored.  K-major B is handled like A (rows of
-  // B past N read zeros).  N-major B columns past N (edge tiles) are clamped
-  // onto the last 8 columns.  Offsets are 32-bit (the host bounds lda and
-  // ldb_k).  ldb_k is the stride between B's rows: K rows for N-major B, N
-  // rows for K-major B.
+  // Each descriptor ends exactly at the last element the tile may use, so a
+  // DMA past it writes zeros and reads no memory: A's descriptor ends at the
+  // tile's last valid row (rows past the expert's count, or past M, cost no
+  // traffic; their results are never stored), B's at the last row of K.
+  // K-major B is handled like A (rows of B past N read zeros).  N-major B
+  // columns past N (edge tiles) are clamped onto the last 8 columns.  Offsets
+  // are 32-bit (the host bounds lda and ldb_k).  ldb_k is the stride between
+  // B's rows: K rows for N-major B, N rows for K-major B.
   auto a_swz = [](int r) {
     return kAChunks == 2 ? (r >> 3) & 1 : kAChunks == 4 ? (r >> 2) & 3 : (r >> 1) & 7;
   };
@@ -380,7 +380,8 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   auto set_sources = [&](const Coords& c) {
     int64_t r0 = c.row_base;
     r0 = r0 < 0 ? 0 : (r0 > p.m ? p.m : r0);
-    const int64_t a_end = r0 < p.m ? ((p.m - 1 - r0) * p.lda + K) * kE : 0;
+    const int64_t r_end = c.row_base + c.rows_valid < p.m ? c.row_base + c.rows_valid : p.m;
+    const int64_t a_end = r0 < r_end ? ((r_end - 1 - r0) * p.lda + K) * kE : 0;
     a_rsrc = make_rsrc4(a_bytes + r0 * p.lda * kE, a_end);
     if constexpr (T::kBKMajor) {
       const int64_t b_end = c.n0 < p.n ? ((p.n - 1 - c.n0) * p.ldb_k + K) * kE : 0;
