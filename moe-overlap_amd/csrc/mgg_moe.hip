@@ -42,29 +42,71 @@ constexpr int kLayoutScanThreads = 1024;
 
 // Pass 2 (one workgroup): offsets[e] = sum of counts of experts below e;
 // hist[b][e] becomes the first position of chunk b's assignments to e
-// (offsets[e] + those of chunks before b), counts[e] the total.
+// (offsets[e] + those of chunks before b), counts[e] the total.  Threads are
+// (part, expert) pairs: with fewer than 1024 experts the chunks of an expert
+// are cut into `parts` ranges summed in parallel, then prefixed in LDS.
+// Loads go out eight chunks at a time.
 __global__ void __launch_bounds__(kLayoutScanThreads)
 layout_scan_kernel(int32_t* hist, int32_t nb, int32_t E, int32_t* counts, int32_t* offsets) {
   __shared__ int32_t s_scan[kLayoutScanThreads];
+  __shared__ int32_t s_part[kLayoutScanThreads];  // [parts][E] range sums, then range bases
   const int tid = threadIdx.x;
-  const int per = (E + kLayoutScanThreads - 1) / kLayoutScanThreads;
-  const int e0 = tid * per;
-  // Within-expert exclusive prefix over chunks; totals per expert.
+  int parts = E > 0 && E < kLayoutScanThreads ? kLayoutScanThreads / E : 1;
+  parts = parts < nb ? parts : (nb > 0 ? nb : 1);
+  const int per = (E + kLayoutScanThreads - 1) / kLayoutScanThreads;  // experts per thread
+  auto chunk_range = [&](int part, int& b0, int& b1) {
+    b0 = (int)((int64_t)part * nb / parts);
+    b1 = (int)((int64_t)(part + 1) * nb / parts);
+  };
+  // Sum (or, with base >= 0, exclusive-prefix in place from base) chunks
+  // [b0, b1) of expert e.
+  auto walk = [&](int e, int b0, int b1, int32_t base) -> int32_t {
+    int32_t run = base < 0 ? 0 : base;
+    for (int b = b0; b < b1; b += 8) {
+      int32_t c[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) c[j] = b + j < b1 ? hist[(int64_t)(b + j) * E + e] : 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (b + j < b1) {
+          if (base >= 0) hist[(int64_t)(b + j) * E + e] = run;
+          run += c[j];
+        }
+      }
+    }
+    return run;
+  };
   int32_t local = 0;
-  for (int i = 0; i < per; ++i) {
-    const int e = e0 + i;
-    if (e < E) {
+  if (parts > 1) {
+    const int e = tid % E, part = tid / E;
+    int b0 = 0, b1 = 0;
+    if (part < parts) {
+      chunk_range(part, b0, b1);
+      s_part[part * E + e] = walk(e, b0, b1, -1);
+    }
+    __syncthreads();
+    if (part == 0) {
       int32_t run = 0;
-      for (int b = 0; b < nb; ++b) {
-        int32_t* h = hist + (int64_t)b * E + e;
-        const int32_t c = *h;
-        *h = run;
+      for (int q = 0; q < parts; ++q) {
+        const int32_t c = s_part[q * E + e];
+        s_part[q * E + e] = run;
         run += c;
       }
       counts[e] = run;
-      local += run;
+      local = run;
+    }
+  } else {
+    for (int i = 0; i < per; ++i) {
+      const int e = tid * per + i;
+      if (e < E) {
+        const int32_t run = walk(e, 0, nb, -1);
+        counts[e] = run;
+        local += run;
+      }
     }
   }
+  // Exclusive scan of the expert totals (thread t holds the total of its
+  // experts; with parts > 1 only the part-0 threads, experts 0..E-1, do).
   s_scan[tid] = local;
   __syncthreads();
   for (int d = 1; d < kLayoutScanThreads; d <<= 1) {
@@ -73,23 +115,36 @@ layout_scan_kernel(int32_t* hist, int32_t nb, int32_t E, int32_t* counts, int32_
     s_scan[tid] += add;
     __syncthreads();
   }
-  int32_t base = s_scan[tid] - local;
-  for (int i = 0; i < per; ++i) {
-    const int e = e0 + i;
-    if (e < E) {
-      offsets[e] = base;
-      for (int b = 0; b < nb; ++b) hist[(int64_t)b * E + e] += base;
-      base += counts[e];
+  const int32_t first = s_scan[tid] - local;  // offset of this thread's first expert
+  if (tid == kLayoutScanThreads - 1) offsets[E] = s_scan[kLayoutScanThreads - 1];
+  if (parts > 1) {
+    const int e = tid % E, part = tid / E;
+    // Thread e is expert e's part-0 thread, so the experts below e sum to s_scan[e - 1].
+    const int32_t off_e = e > 0 ? s_scan[e - 1] : 0;
+    if (part == 0) offsets[e] = off_e;
+    if (part < parts) {
+      int b0 = 0, b1 = 0;
+      chunk_range(part, b0, b1);
+      walk(e, b0, b1, off_e + s_part[part * E + e]);
+    }
+  } else {
+    int32_t base = first;
+    for (int i = 0; i < per; ++i) {
+      const int e = tid * per + i;
+      if (e < E) {
+        offsets[e] = base;
+        walk(e, 0, nb, base);
+        base += counts[e];
+      }
     }
   }
-  if (tid == kLayoutScanThreads - 1) offsets[E] = s_scan[kLayoutScanThreads - 1];
 }
 
-// Pass 3 (one wave per chunk, 64 assignments at a time in order): an
-// assignment's position is its chunk's base for its expert plus the number of
-// earlier assignments of the chunk to the same expert, so positions are stable
-// (assignment order within each expert).  Lanes sharing an expert are grouped
-// with ballots, one round per distinct expert in the 64.
+// Pass 3 for any expert count (one wave per chunk, 64 assignments at a time
+// in order): an assignment's position is its chunk's base for its expert plus
+// the number of earlier assignments of the chunk to the same expert, so
+// positions are stable (assignment order within each expert).  Lanes sharing
+// an expert are grouped with ballots, one round per distinct expert in the 64.
 template <class In>
 __global__ void __launch_bounds__(64)
 layout_scatter_kernel(const In* idx, int64_t A, int32_t top_k, int32_t E, const int32_t* hist,
@@ -133,6 +188,64 @@ layout_scatter_kernel(const In* idx, int64_t A, int32_t top_k, int32_t E, const 
     __syncthreads();  // every lane has read its base before the bases move on
     if (valid && last) s_base[e] += rank + 1;
     __syncthreads();
+  }
+}
+
+// Pass 3 for up to kMaxWideExperts experts: a chunk's kLayoutChunk
+// assignments take one lane each (kLayoutChunk / 64 waves).  Each wave ranks
+// its 64 assignments per expert with ballots and records its per-expert
+// counts in LDS; a prefix over the waves, per expert, then gives each wave's
+// base.  Positions are those of layout_scatter_kernel (assignment order
+// within each expert), with every assignment in flight at once.
+constexpr int kWideWaves = kLayoutChunk / 64;
+constexpr int kMaxWideExperts = 1024;  // [kWideWaves][E] int32 counters in 64 KiB of LDS
+
+template <class In>
+__global__ void __launch_bounds__(kLayoutChunk)
+layout_scatter_wide_kernel(const In* idx, int64_t A, int32_t top_k, int32_t E,
+                           const int32_t* hist, int32_t* slot_pos, int32_t* token_index,
+                           int32_t* row_assign) {
+  extern __shared__ int32_t s_cnt[];  // [kWideWaves][E]: counts, then bases
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  for (int i = tid; i < kWideWaves * E; i += kLayoutChunk) s_cnt[i] = 0;
+  __syncthreads();
+  const int64_t a = (int64_t)blockIdx.x * kLayoutChunk + tid;
+  int32_t e = -1;
+  if (a < A) {
+    const int64_t v = (int64_t)idx[a];
+    e = (v >= 0 && v < E) ? (int32_t)v : -1;
+  }
+  const bool valid = e >= 0;
+  uint64_t todo = __ballot(valid);
+  int32_t rank = 0;
+  while (todo != 0) {
+    const int leader = __builtin_ctzll(todo);
+    const int32_t el = __builtin_amdgcn_readlane(e, leader);
+    const bool mine = valid && e == el;
+    const uint64_t m = __ballot(mine);
+    if (mine) rank = __builtin_popcountll(m & ((1ull << lane) - 1ull));
+    if (lane == leader) s_cnt[w * E + el] = __builtin_popcountll(m);
+    todo &= ~m;
+  }
+  __syncthreads();
+  for (int x = tid; x < E; x += kLayoutChunk) {
+    int32_t run = hist[(int64_t)blockIdx.x * E + x];
+    for (int v = 0; v < kWideWaves; ++v) {
+      const int32_t c = s_cnt[v * E + x];
+      s_cnt[v * E + x] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  if (valid) {
+    const int32_t pos = s_cnt[w * E + e] + rank;
+    slot_pos[a] = pos;
+    token_index[pos] = (int32_t)(a / top_k);
+    row_assign[pos] = (int32_t)a;
+  } else if (a < A) {
+    slot_pos[a] = -1;
   }
 }
 
@@ -262,7 +375,19 @@ int launch_dispatch_layout(const void* topk_idx, int idx_type, int64_t num_token
                      (int32_t)nb, num_experts, counts, offsets);
   if (hipError_t err = hipGetLastError(); err != hipSuccess)
     return hip_error(err, "layout scan launch");
-  if (nb > 0) {
+  if (nb > 0 && num_experts <= kMaxWideExperts) {
+    const size_t wide_lds = (size_t)kWideWaves * lds;
+    if (idx_type == MGG_INT64)
+      hipLaunchKernelGGL(layout_scatter_wide_kernel<int64_t>, dim3((unsigned)nb),
+                         dim3(kLayoutChunk), wide_lds, stream, (const int64_t*)topk_idx, A, top_k,
+                         num_experts, hist, slot_pos, token_index, row_assign);
+    else
+      hipLaunchKernelGGL(layout_scatter_wide_kernel<int32_t>, dim3((unsigned)nb),
+                         dim3(kLayoutChunk), wide_lds, stream, (const int32_t*)topk_idx, A, top_k,
+                         num_experts, hist, slot_pos, token_index, row_assign);
+    if (hipError_t err = hipGetLastError(); err != hipSuccess)
+      return hip_error(err, "layout scatter launch");
+  } else if (nb > 0) {
     if (idx_type == MGG_INT64)
       hipLaunchKernelGGL(layout_scatter_kernel<int64_t>, dim3((unsigned)nb), dim3(64), lds, stream,
                          (const int64_t*)topk_idx, A, top_k, num_experts, hist, slot_pos,
