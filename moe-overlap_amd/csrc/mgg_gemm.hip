@@ -136,16 +136,20 @@ __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_pr
       local += (int32_t)tiles;
     }
   }
-  s_scan[tid] = local;
-  __syncthreads();
-  // Hillis-Steele inclusive scan over the NT per-thread sums.
-  for (int d = 1; d < NT; d <<= 1) {
-    const int32_t add = tid >= d ? s_scan[tid - d] : 0;
-    __syncthreads();
-    s_scan[tid] += add;
-    __syncthreads();
+  // Inclusive scan of the NT per-thread sums: within each wave by lane
+  // shuffles, then across the NT/64 wave totals (one barrier).
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  int32_t incl = local;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int32_t y = __shfl_up(incl, d);
+    if (lane >= d) incl += y;
   }
-  int32_t base = s_scan[tid] - local;
+  if (lane == 63) s_scan[wave] = incl;
+  __syncthreads();
+  for (int v = 0; v < wave; ++v) incl += s_scan[v];
+  int32_t base = incl - local;
   for (int i = 0; i < per; ++i) {
     const int e = e0 + i;
     if (e < E) {
@@ -156,7 +160,7 @@ __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_pr
     }
   }
   if (tid == NT - 1) {
-    s_prefix[E] = s_scan[NT - 1];
+    s_prefix[E] = incl;
     if (s_offs != nullptr) s_offs[E] = p.offsets[E];
   }
   __syncthreads();
@@ -634,7 +638,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     __syncthreads();
     // The next tile's ticket, taken after the first wait so that this
     // wave's first DMA wait does not also wait for the atomic.
-    if (take_ticket && tid == 0) ticket = atomicAdd(p.counter, 1);
+    if (take_ticket && tid == 0) ticket = G + atomicAdd(p.counter, 1);
     if (nk > 0) {
       read_kstep(0, 0, 0, 0);
       read_kstep(0, 0, 0, 1);
@@ -732,7 +736,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   // Blocking ticket (used for the first item and to skip a caller queue's
   // invalid items): the leader takes it and broadcasts it through LDS.
   auto take_ticket_now = [&]() -> int32_t {
-    if (tid == 0) *s_item = atomicAdd(p.counter, 1);
+    if (tid == 0) *s_item = G + atomicAdd(p.counter, 1);
     __syncthreads();
     const int32_t t = *s_item;
     __syncthreads();
@@ -830,28 +834,27 @@ grouped_gemm_kernel(GemmParams p) {
   int v = blockIdx.x;
   if (p.remap_xcd && (G & 7) == 0) v = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
 
-  // Striped: items v, v+G, v+2G, ...  Atomic: tickets from the global
-  // counter, the first one taken here (the leader broadcasts it via LDS).
-  int32_t first = v;
-  if (p.atomic) {
-    if (tid == 0) s_item = atomicAdd(p.counter, 1);
-    __syncthreads();
-    first = s_item;
-    __syncthreads();
-  }
+  // Striped: items v, v+G, v+2G, ...  Atomic: worker b's first item is b
+  // (the first G items need no ticket), then tickets t of the global counter
+  // stand for items G + t; a worker stops at its first ticket past the queue.
+  const int32_t first = p.atomic ? (int32_t)blockIdx.x : v;
   run_worker<BM, BN, SBK, NSTAGE, NW, T, EPI>(p, W, first, n_tiles, s_prefix,
                                          (kOffsLds && p.num_work < 0) ? s_offs : nullptr,
                                          &s_item, lds, s_scale);
   if (!p.atomic) return;
   // Every worker has fetched its final (out-of-range) ticket before adding to
-  // `done`, so the last one to arrive reads the final count (W + G when no
-  // worker stops early), hands it to the caller's work_counter and returns
-  // both library counters to zero for the next launch on this stream.
+  // `done`, so the last one to arrive reads the final count, returns both
+  // library counters to zero for the next launch on this stream, and hands
+  // the caller's work_counter the value the reference's single counter ends
+  // at, W + G (every item dequeued once, one over-fetch per worker).  Here
+  // items past the first G take one ticket each and every worker that had a
+  // first item over-fetches once, so the counter ends at W and the value
+  // handed over is final + G.
   if (tid == 0) {
     if (atomicAdd(p.done, 1) == G - 1) {
       const int32_t final_count = atomicExch(p.counter, 0);
       atomicExch(p.done, 0);
-      if (p.report != nullptr) atomicExch(p.report, final_count);
+      if (p.report != nullptr) atomicExch(p.report, final_count + G);
     }
   }
 }
