@@ -260,6 +260,8 @@ def persistent_grouped_gemm(
         raise ValueError("b_expert dtype should match a_cat dtype.")
     if queue not in ("device", "prebuilt"):
         raise ValueError("queue must be 'device' or 'prebuilt'.")
+    if queue == "device" and b_expert.size(0) > _nat.MAX_DEVICE_QUEUE_EXPERTS:
+        queue = "prebuilt"  # the device-derived queue keeps its tile prefix in LDS
 
     m_total, k_size = a_cat.shape
     num_experts, _, n_size = b_expert.shape

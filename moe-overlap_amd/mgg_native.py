@@ -25,6 +25,10 @@ MGG_DTYPE_FP16 = 1
 MGG_DTYPE_FP8_E4M3 = 2
 MGG_INT32 = 0
 MGG_INT64 = 1
+# Largest expert count for which the kernels derive the work queue on the
+# device (the per-expert tile prefix lives in LDS; kMaxLdsExpertsGemm).
+MAX_DEVICE_QUEUE_EXPERTS = 2048
+
 MGG_EPI_NONE = 0
 MGG_EPI_GELU = 1
 MGG_EPI_SWIGLU = 2

@@ -189,6 +189,24 @@ def test_striped_with_few_workers(cuda_device):
         assert_parity(c, a, b, offs, 96)
 
 
+@pytest.mark.parametrize("num_experts", [2048, 2500])
+def test_many_experts(cuda_device, num_experts):
+    """2048 experts is the largest count whose queue the kernel derives in
+    LDS; beyond it the drop-in builds the queue on the host (the reference's
+    path) without being asked."""
+    rng = np.random.default_rng(num_experts)
+    counts = rng.integers(0, 40, num_experts).tolist()
+    counts[7] = 300  # one expert spans two 256-row tiles
+    a, b, offs = make_inputs(counts, 64, 64, torch.bfloat16, cuda_device, seed=3)
+    for blocks in [(64, 64), (256, 256)]:
+        for atomic in (False, True):
+            log(f"E={num_experts} blocks={blocks} atomic={atomic}")
+            c = gg.persistent_grouped_gemm(a, b, offs, block_m=blocks[0], block_n=blocks[1],
+                                           use_atomic_queue=atomic)
+            torch.cuda.synchronize()
+            assert_parity(c, a, b, offs, 64)
+
+
 def test_odd_shapes_are_padded(cuda_device):
     a, b, offs = make_inputs([17, 0, 40], 50, 37, torch.bfloat16, cuda_device)
     c = gg.persistent_grouped_gemm(a, b, offs)
