@@ -39,8 +39,10 @@ KERNEL_NAME = "grouped_gemm_kernel<256,256,64,2,8,Bf16,0>"
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
+    # The card idles at a low clock and takes tens of milliseconds of work to reach its steady
+    # clock, so the default warmup (~30 ms of launches) ends in steady state.
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--workload", default="uniform",
                    choices=["uniform", "skewed", "cpu_plumbing", "expert_mlp", "fp8"],
                    help="uniform (the metric's config), skewed, cpu_plumbing; expert_mlp and fp8 "
