@@ -192,53 +192,58 @@ def fp8_summary(dev, steps: int = 20):
     return out
 
 
-def overlap_summary(case, offs, dev, steps: int = 10):
-    """What one GPU shows of the multi-GPU overlap design: (1) the GEMM with
-    CUs held back for communication kernels (num_sms < 256, the analogue of
-    the reference's DeepEP SM reservation), (2) the GEMM on one stream while a
-    copy of the next micro-batch's tokens runs on another stream (the local
-    memory traffic of a dispatch), against the two back to back."""
+def overlap_summary(case, offs, dev, iters: int = 60):
+    """What one GPU shows of the multi-GPU overlap design, per launch over a pipeline of
+    `iters` iterations timed by the host clock: (1) the GEMM with CUs held back for
+    communication kernels (num_sms < 256, the analogue of the reference's DeepEP SM
+    reservation); (2) each iteration's GEMM on one created stream while a copy of the
+    micro-batch's tokens (the local memory traffic of a dispatch, 2 x 32 MiB) runs on
+    another, joined at the iteration's end, against the two back to back on one stream.
+    Both streams are created streams: the legacy default stream would serialise them."""
     import torch
 
     import grouped_gemm as gg
 
-    out = {"cu_reservation_ms": {}}
-    for sms in (256, 240, 224, 192):
-        fn = lambda: gg.persistent_grouped_gemm(case.a, case.b, offs, num_sms=sms)
-        event_times_ms(fn, 2)
-        out["cu_reservation_ms"][str(sms)] = round(median(event_times_ms(fn, steps)), 4)
-    # dispatch-sized copy: the tokens of a micro-batch (M x K bf16, 32 MiB), moved twice
-    # (send and receive buffers of an all-to-all on one rank)
     src = torch.empty_like(case.a)
     dst = torch.empty_like(case.a)
-    side = torch.cuda.Stream(device=dev)
-    main = torch.cuda.current_stream(dev)
+    s_main = torch.cuda.Stream(device=dev)
+    s_side = torch.cuda.Stream(device=dev)
 
     def copies():
         dst.copy_(src)
         src.copy_(dst)
 
-    def serial():
-        gg.persistent_grouped_gemm(case.a, case.b, offs, num_sms=224)
-        copies()
+    def pipeline(sms, mode, n):
+        for _ in range(n):
+            if mode != "copy":
+                with torch.cuda.stream(s_main):
+                    gg.persistent_grouped_gemm(case.a, case.b, offs, num_sms=sms)
+            if mode == "serial":
+                with torch.cuda.stream(s_main):
+                    copies()
+            elif mode in ("overlapped", "copy"):
+                with torch.cuda.stream(s_side):
+                    copies()
+                s_main.wait_stream(s_side)
+                s_side.wait_stream(s_main)
 
-    def overlapped(sms):
-        # the GEMM is submitted first so that its workgroups take their CUs before the
-        # copy's many small workgroups fill the rest
-        side.wait_stream(main)
-        gg.persistent_grouped_gemm(case.a, case.b, offs, num_sms=sms)
-        with torch.cuda.stream(side):
-            copies()
-        main.wait_stream(side)
+    def per_iter_us(sms, mode):
+        pipeline(sms, mode, 20)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        pipeline(sms, mode, iters)
+        torch.cuda.synchronize()
+        return round((time.perf_counter() - t0) / iters * 1e6, 1)
 
-    for name, fn in (("serial_ms", serial), ("overlapped_ms", lambda: overlapped(224)),
-                     ("overlapped_all_cus_ms", lambda: overlapped(256))):
-        event_times_ms(fn, 2)
-        out[name] = round(median(event_times_ms(fn, steps)), 4)
-    event_times_ms(copies, 2)
-    out["copy_alone_ms"] = round(median(event_times_ms(copies, steps)), 4)
-    out["note"] = ("GEMM at num_sms=224 (32 CUs left for the copy), copy = 2 x 32 MiB device "
-                   "copies on a second stream of default priority")
+    out = {"unit": "µs per iteration"}
+    for sms in (256, 240, 224, 192):
+        out[f"gemm_alone_{sms}"] = per_iter_us(sms, "gemm")
+    for sms in (256, 224):
+        out[f"serial_{sms}"] = per_iter_us(sms, "serial")
+        out[f"overlapped_{sms}"] = per_iter_us(sms, "overlapped")
+    out["copy_alone"] = per_iter_us(0, "copy")
+    out["note"] = ("copy = 2 x 32 MiB device copies; overlapped = GEMM and copy on two created "
+                   "streams of default priority, joined every iteration")
     return out
 
 
