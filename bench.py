@@ -33,7 +33,7 @@ METRIC = "grouped GEMM TFLOP/s + % bf16 MFMA peak, E=16 512 tok/expert K2048 N40
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0
 PEAK_FP8_TFLOPS = 5033.2  # MI355X dense fp8 MFMA
-KERNEL_NAME = "grouped_gemm_kernel<256,256,64,2,8,Bf16,0>"
+KERNEL_NAME = "grouped_gemm_kernel<256,256,32,4,8,Bf16,0>"
 
 
 def parse_args():

@@ -18,9 +18,13 @@
 #include "mgg.h"
 #include "mgg_internal.h"
 
+// 256x256 bf16/fp16 tiles: 32-deep K stages in a ring of four (128 KiB),
+// three stages in flight while one is multiplied.  A ring of two 64-deep
+// stages (one in flight) moves the same bytes per barrier pair but measured
+// 5-7% slower: the K loop is bound by bytes in flight per CU.
 #ifndef MGG_SBK256
-#define MGG_SBK256 64
-#define MGG_NS256 2
+#define MGG_SBK256 32
+#define MGG_NS256 4
 #endif
 #ifndef MGG_NW256
 #define MGG_NW256 8
@@ -871,9 +875,10 @@ int launch_typed(int block_m, int block_n, const GemmParams& p, int workers, hip
                        dim3(NW_ * 64), 0, stream, p);                                           \
     return MGG_OK;                                                                              \
   }
-  // (tile, K per stage, LDS stages, waves): 128-byte A rows (64-wide K
-  // stages), as many stages as the LDS budget holds.  Fused epilogues are
-  // compiled for the 256x256 and 128x128 tiles (two 32-column blocks per wave).
+  // (tile, K per stage, LDS stages, waves): 64-wide K stages (128-byte A
+  // rows) and as many stages as the LDS budget holds, except the 256x256
+  // tile (see MGG_SBK256).  Fused epilogues are compiled for the 256x256 and
+  // 128x128 tiles (two 32-column blocks per wave).
   MGG_CASE(256, 256, MGG_SBK256, MGG_NS256, MGG_NW256)
   MGG_CASE(128, 128, 64, 4, 4)
   if constexpr (EPI == kEpiNone) {
