@@ -8,13 +8,14 @@
 // A[off_e + tm*BM + i, k] * B[e, k, tn*BN + j] (:36-98): rows past the expert's
 // count are never stored, fp32 accumulation, output rounded to the input type.
 //
-// Data path (run_tile): K advances in stages; A [BM x SBK] and B [SBK x BN]
+// Data path (run_worker): K advances in stages; A [BM x SBK] and B [SBK x BN]
 // move HBM -> LDS by buffer DMA (16 bytes per lane, no VGPR staging), several
 // stages ahead of the one being multiplied.  A fragments are 128-bit LDS reads;
 // B stays N-contiguous in LDS and is read with the gfx950 transposing read
 // ds_read_b64_tr_b16, so no transpose is ever done in registers.  The MFMA is
-// v_mfma_f32_32x32x16_{bf16,f16}; it computes C^T = B^T A^T so each lane ends
-// up with 4 consecutive N values of a row, stored as one 8-byte write.
+// v_mfma_f32_32x32x16_{bf16,f16} (fp8: v_mfma_f32_32x32x64_f8f6f4 with K-major
+// B); it computes C^T = B^T A^T so each lane ends up with 4 consecutive N
+// values of a row, and lanes l and l+32 swap halves so each stores 16 bytes.
 #include "mgg.h"
 #include "mgg_internal.h"
 
@@ -239,15 +240,16 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // arguments, and every branch below that guards a barrier, are uniform across
 // the workgroup.
 //
-// K advances in stages of SBK (16, 32 or 64); NSTAGE stages rotate through LDS.
-// A stage holds A [BM x SBK] as BM rows of 2*SBK bytes and B [SBK x BN] in
-// its global layout (K rows of BN contiguous N values); both arrive by DMA,
-// NSTAGE-1 stages ahead of the one being multiplied.  16-byte chunks are
+// K advances in stages of SBK elements; NSTAGE stages rotate through LDS.
+// A stage holds A [BM x SBK] as BM rows of SBK*kElem bytes and B [SBK x BN]
+// in its global layout (K rows of BN contiguous N values; K-major fp8 B is
+// stored like A); both arrive by DMA, NSTAGE-1 stages ahead of the one being
+// multiplied.  16-byte chunks are
 // XOR-swizzled on the global side so that the fragment reads below are
 // bank-conflict free:
-//   A row r, chunk c  -> physical chunk c ^ ((r >> 3) & 1)    (SBK == 16)
-//                                        c ^ ((r >> 2) & 3)    (SBK == 32)
-//                                        c ^ ((r >> 1) & 7)    (SBK == 64)
+//   A row r, chunk c  -> physical chunk c ^ ((r >> 3) & 1)    (32-byte rows)
+//                                        c ^ ((r >> 2) & 3)    (64-byte rows)
+//                                        c ^ ((r >> 1) & 7)    (128-byte rows)
 //   B row k, chunk c  -> physical chunk c ^ 4*(k & 3)          (BN >= 128)
 //                                        c ^ 4*((k >> 1) & 1)  (BN == 64)
 // A fragments are ds_read_b128 (8 consecutive K of one row).  B fragments use
