@@ -840,10 +840,11 @@ grouped_gemm_kernel(GemmParams p) {
   int v = blockIdx.x;
   if (p.remap_xcd && (G & 7) == 0) v = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
 
-  // Striped: items v, v+G, v+2G, ...  Atomic: worker b's first item is b
-  // (the first G items need no ticket), then tickets t of the global counter
-  // stand for items G + t; a worker stops at its first ticket past the queue.
-  const int32_t first = p.atomic ? (int32_t)blockIdx.x : v;
+  // Striped: items v, v+G, v+2G, ...  Atomic: worker v's first item is v
+  // (the first G items need no ticket and start in the striped schedule's
+  // XCD-aware placement), then tickets t of the global counter stand for
+  // items G + t; a worker stops at its first ticket past the queue.
+  const int32_t first = v;
   run_worker<BM, BN, SBK, NSTAGE, NW, T, EPI>(p, W, first, n_tiles, s_prefix,
                                          (kOffsLds && p.num_work < 0) ? s_offs : nullptr,
                                          &s_item, lds, s_scale);
