@@ -104,6 +104,42 @@ def test_small_ragged_parity_all_modes(cuda_device, case, dtype):
                 assert torch.equal(got, ref), (blocks, atomic, queue)
 
 
+def random_case(seed):
+    """A seeded random problem: 1-9 experts with counts in [0, 600] (some
+    empty, some a single row), K in [8, 1200] and N in [8, 700] (multiples of
+    8, so tails inside a K stage and a column tile are common)."""
+    rng = np.random.default_rng(seed)
+    e = int(rng.integers(1, 10))
+    counts = rng.integers(0, 601, e)
+    counts[rng.random(e) < 0.25] = 0
+    counts[rng.random(e) < 0.15] = 1
+    k = 8 * int(rng.integers(1, 151))
+    n = 8 * int(rng.integers(1, 88))
+    blocks = [(256, 256), (128, 128), (256, 128), (128, 256), (64, 64), (64, 128), (128, 64),
+              (256, 64), (64, 256)][int(rng.integers(0, 9))]
+    return counts.tolist(), k, n, blocks
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_shapes_match_oracle(cuda_device, seed):
+    counts, k, n, blocks = random_case(seed)
+    log(f"random seed={seed} counts={counts} K={k} N={n} blocks={blocks}")
+    dtype = torch.bfloat16 if seed % 2 == 0 else torch.float16
+    a, b, offs = make_inputs(counts, k, n, dtype, cuda_device, seed=100 + seed, extra_rows=seed % 3)
+    outs = []
+    for atomic in (False, True):
+        for queue in ("device", "prebuilt"):
+            c = gg.persistent_grouped_gemm(a, b, offs, block_m=blocks[0], block_n=blocks[1],
+                                           use_atomic_queue=atomic, queue=queue,
+                                           num_sms=int(7 + 37 * seed) % 300 + 1)
+            torch.cuda.synchronize()
+            outs.append(c)
+    assert_parity(outs[0], a, b, offs, k)
+    mask = torch.from_numpy(covered_rows(offs)).to(cuda_device)
+    for c in outs[1:]:
+        assert torch.equal(c[: mask.numel()][mask], outs[0][: mask.numel()][mask])
+
+
 def test_cpu_plumbing_config_in_bf16(cuda_device):
     case = workloads.make_case("cpu_plumbing", device="cpu", dtype=torch.bfloat16)
     offs = gg.expert_offsets_from_recv_counts(case.counts, device=cuda_device)
