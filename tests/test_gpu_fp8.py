@@ -68,6 +68,29 @@ def test_fp8_small_ragged(cuda_device, block_m, block_n, atomic):
     assert_close_fp8(c, a, sa, b, sb, offs)
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_fp8_random_shapes(cuda_device, seed):
+    """Seeded random fp8 problems: 1-7 experts (some empty or one row), K and N
+    that need padding (K to 16, N to 8) half the time, both tiles, both
+    schedules, bitwise-equal across schedules."""
+    rng = np.random.default_rng(1000 + seed)
+    e = int(rng.integers(1, 8))
+    counts = rng.integers(0, 500, e)
+    counts[rng.random(e) < 0.25] = 0
+    counts[rng.random(e) < 0.15] = 1
+    k = int(rng.integers(1, 90)) * (16 if seed % 2 == 0 else 7)
+    n = int(rng.integers(1, 60)) * (8 if seed % 2 == 0 else 5)
+    bm = (256, 128)[seed % 2]
+    log(f"fp8 random seed={seed} counts={counts.tolist()} K={k} N={n} block_m={bm}")
+    a, sa, b, sb, offs = fp8_inputs(counts.tolist(), k, n, seed=seed, device=cuda_device)
+    outs = [gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, block_m=bm, block_n=128,
+                                       use_atomic_queue=atomic, a_scale=sa, b_scale=sb,
+                                       num_sms=int(rng.integers(1, 300)))
+            for atomic in (False, True)]
+    assert_close_fp8(outs[0], a, sa, b, sb, offs)
+    assert torch.equal(outs[0], outs[1])
+
+
 def test_fp8_padded_shapes_and_b_layouts(cuda_device):
     log("fp8 padded")
     counts = [9, 70, 0, 33]
