@@ -47,7 +47,9 @@ def parse_args():
                    choices=["uniform", "skewed", "cpu_plumbing", "expert_mlp", "fp8"],
                    help="uniform (the metric's config), skewed, cpu_plumbing; expert_mlp and fp8 "
                         "time the BASELINE expert-MLP forward / fp8 GEMM configs instead")
-    p.add_argument("--mode", default="atomic", choices=["atomic", "striped"])
+    # striped by default, as the reference's benchmark (src/bench_triton_grouped_gemm.py:28-32:
+    # --atomic-queue is opt-in); the comparison below times both schedules either way
+    p.add_argument("--mode", default="striped", choices=["atomic", "striped"])
     p.add_argument("--block-m", type=int, default=256)
     p.add_argument("--block-n", type=int, default=256)
     p.add_argument("--num-sms", type=int, default=None)
@@ -122,7 +124,7 @@ def expert_mlp_summary(dev, steps: int = 10):
     case.w_gate = case.w_up = None
     fwd = lambda: mlp.expert_mlp_forward(case.x, case.topk_idx, case.topk_weight, w1, case.w2,
                                          "swiglu")
-    event_times_ms(fwd, 3)
+    event_times_ms(fwd, 30)  # ~30 ms of work: the card back at its steady clock after the set-up
     t_fwd = median(event_times_ms(fwd, steps))
     lay = mlp.dispatch_layout(case.topk_idx, case.experts)
     xp = mlp.permute_tokens(case.x, lay)
@@ -146,7 +148,7 @@ def expert_mlp_summary(dev, steps: int = 10):
            "forward_tflops": round(case.flops / (t_fwd * 1e-3) / 1e12, 1),
            "launch_ms_median": {}}
     for name, fn in parts.items():
-        event_times_ms(fn, 2)
+        event_times_ms(fn, 20)
         out["launch_ms_median"][name] = round(median(event_times_ms(fn, steps)), 4)
     lm = out["launch_ms_median"]
     out["up_gemm_tflops"] = round(up_flops / (lm["up_gemm_swiglu"] * 1e-3) / 1e12, 1)
@@ -178,7 +180,7 @@ def fp8_summary(dev, steps: int = 20):
             fn = lambda: gg.persistent_grouped_gemm(case.a, b_kn, offs, block_m=bm, block_n=bn,
                                                     use_atomic_queue=mode == "atomic",
                                                     a_scale=case.a_scale, b_scale=case.b_scale)
-            event_times_ms(fn, 3)
+            event_times_ms(fn, 100)
             t = median(event_times_ms(fn, steps))
             r = {"kernel_ms_median": round(t, 4),
                  "tflops": round(case.flops / (t * 1e-3) / 1e12, 1),
@@ -421,12 +423,10 @@ def main():
 
     extra = {}
     if not args.no_compare:
-        # Cache-cold launches: a 512 MiB write evicts L2 and the 256 MB MALL.
-        scratch = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
-        cold = event_times_ms(step, 10, flush=lambda: scratch.fill_(1.0))
-        extra["cold_kernel_ms_median"] = round(median(cold), 4)
-        extra["cold_tflops"] = round(flops / (median(cold) * 1e-3) / 1e12, 1)
-        del scratch
+        # The other BASELINE configs first, while the card is at its steady clock (the legs below
+        # load it for seconds; its clock sags under sustained load).
+        extra["expert_mlp"] = expert_mlp_summary(dev)
+        extra["fp8"] = fp8_summary(dev)
         sched = {}
         for wl in ("uniform", "skewed"):
             cs = case if wl == args.workload else workloads.make_case(wl, device=dev)
@@ -435,8 +435,8 @@ def main():
                 fn = lambda: gg.persistent_grouped_gemm(
                     cs.a, cs.b, o, num_sms=args.num_sms, block_m=args.block_m,
                     block_n=args.block_n, use_atomic_queue=(mode == "atomic"))
-                event_times_ms(fn, 3)
-                t = event_times_ms(fn, 20)
+                event_times_ms(fn, 100)  # steady clock before timing each schedule
+                t = event_times_ms(fn, 40)
                 sched[f"{wl}_{mode}"] = {
                     "kernel_ms_median": round(median(t), 4), "kernel_ms_min": round(min(t), 4),
                     "tflops": round(cs.flops / (median(t) * 1e-3) / 1e12, 1)}
@@ -450,8 +450,12 @@ def main():
         extra["torch_loop_gpu_ms_median"] = round(median(tl), 4)
         extra["torch_loop_gpu_tflops"] = round(flops / (median(tl) * 1e-3) / 1e12, 1)
         extra["overlap"] = overlap_summary(case, offs, dev)
-        extra["expert_mlp"] = expert_mlp_summary(dev)
-        extra["fp8"] = fp8_summary(dev)
+        # Cache-cold launches: a 512 MiB write evicts L2 and the 256 MB MALL.
+        scratch = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
+        cold = event_times_ms(step, 10, flush=lambda: scratch.fill_(1.0))
+        extra["cold_kernel_ms_median"] = round(median(cold), 4)
+        extra["cold_tflops"] = round(flops / (median(cold) * 1e-3) / 1e12, 1)
+        del scratch
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(case, args.cpu_seconds)
 
