@@ -179,6 +179,34 @@ def test_expert_mlp_small_matches_oracle(cuda_device, activation):
     assert np.sqrt((err ** 2).mean() / max((ref ** 2).mean(), 1e-30)) <= 1e-2
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_expert_mlp_random_shapes(cuda_device, seed):
+    """Seeded random routed MLPs (tokens, top-k, experts, hidden and FFN sizes,
+    masked slots, both activations, both tile sizes) against the oracle."""
+    rng = np.random.default_rng(200 + seed)
+    T = int(rng.integers(1, 700))
+    k = int(rng.integers(1, 5))
+    E = int(rng.integers(1, 20))
+    H = 64 * int(rng.integers(1, 9))
+    F = 64 * int(rng.integers(1, 9))
+    activation = ("gelu", "swiglu")[seed % 2]
+    block = (128, 256)[(seed // 2) % 2]
+    log(f"mlp random seed={seed} T={T} k={k} E={E} H={H} F={F} {activation} block={block}")
+    idx, w = random_routing(T, k, E, masked_every=int(rng.integers(0, 6)), seed=seed)
+    gen = torch.Generator().manual_seed(300 + seed)
+    x = torch.randn(T, H, generator=gen).to(torch.bfloat16)
+    w1 = (torch.randn(E, H, 2 * F if activation == "swiglu" else F, generator=gen) / math.sqrt(H)).to(torch.bfloat16)
+    w2 = (torch.randn(E, F, H, generator=gen) / math.sqrt(F)).to(torch.bfloat16)
+    got = mlp.expert_mlp_forward(x.to(cuda_device), idx.to(cuda_device), w.to(cuda_device),
+                                 w1.to(cuda_device), w2.to(cuda_device), activation,
+                                 block=block).float().cpu().numpy()
+    ref = mo.expert_mlp(x.float().numpy(), idx.numpy(), w.numpy(), w1.float().numpy(),
+                        w2.float().numpy(), activation)
+    err = np.abs(got - ref)
+    assert err.max() <= 2 * tol(F), err.max()
+    assert np.sqrt((err ** 2).mean() / max((ref ** 2).mean(), 1e-30)) <= 1e-2
+
+
 def test_expert_mlp_baseline_config(cuda_device):
     """BASELINE expert-MLP config (8192 tokens, top-2 of 16, H 2048, SwiGLU F
     4096) against an fp32 torch computation of the same routed MLP."""
