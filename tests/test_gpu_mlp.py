@@ -149,6 +149,38 @@ def test_fused_epilogue_gemm(cuda_device, activation, block, atomic):
         assert err <= 2 * tol(K), (activation, block, s, err)
 
 
+@pytest.mark.parametrize("activation", ["gelu", "swiglu"])
+def test_fp16_epilogues_and_mlp(cuda_device, activation):
+    """The fp16 instantiations of the fused epilogues, and the routed MLP in
+    fp16 (same bounds as bf16; fp16's finer mantissa only tightens them)."""
+    log(f"fp16 {activation}")
+    counts = [70, 0, 301, 9]
+    K, N = 512, 256
+    gen = torch.Generator().manual_seed(21)
+    M = sum(counts)
+    a = torch.randn(M, K, generator=gen).to(torch.float16).to(cuda_device)
+    b = (torch.randn(len(counts), K, N, generator=gen) / math.sqrt(K)).to(torch.float16).to(cuda_device)
+    offs = torch.tensor([0] + list(np.cumsum(counts)), dtype=torch.int32, device=cuda_device)
+    cols = N // 2 if activation == "swiglu" else N
+    for block in (128, 256):
+        c = mlp._grouped_gemm_ex(a, b, offs, mlp._EPILOGUES[activation], cols, None, block, True)
+        assert c.dtype == torch.float16
+        for s0, t0, h in fp32_epilogue_ref(a, b, offs, activation):
+            assert (c.float()[s0:t0] - h).abs().max().item() <= 2 * tol(K)
+    T, k, E, H, F = 150, 2, 4, 128, 128
+    idx, w = random_routing(T, k, E, masked_every=7, seed=8)
+    x = torch.randn(T, H, generator=gen).to(torch.float16)
+    w1 = (torch.randn(E, H, 2 * F if activation == "swiglu" else F, generator=gen) / math.sqrt(H)).to(torch.float16)
+    w2 = (torch.randn(E, F, H, generator=gen) / math.sqrt(F)).to(torch.float16)
+    got = mlp.expert_mlp_forward(x.to(cuda_device), idx.to(cuda_device), w.to(cuda_device),
+                                 w1.to(cuda_device), w2.to(cuda_device), activation)
+    assert got.dtype == torch.float16
+    ref = mo.expert_mlp(x.float().numpy(), idx.numpy(), w.numpy(), w1.float().numpy(),
+                        w2.float().numpy(), activation)
+    err = np.abs(got.float().cpu().numpy() - ref)
+    assert err.max() <= 2 * tol(F), err.max()
+
+
 def test_fused_epilogue_rejects_unsupported_shapes(cuda_device):
     a = torch.zeros(64, 64, dtype=torch.bfloat16, device=cuda_device)
     b = torch.zeros(1, 64, 96, dtype=torch.bfloat16, device=cuda_device)
