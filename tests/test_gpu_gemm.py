@@ -280,6 +280,42 @@ def test_rows_outside_experts_are_not_written(cuda_device):
         assert float(np.abs(c[2:16].float().cpu().numpy() - want).max()) <= tol(64)
 
 
+def test_caller_queue_with_invalid_items(cuda_device):
+    """A caller-built queue may hold items that cover no rows: a tile_m past the
+    expert's rows or a tile_n past N (the reference's masks make those no-ops,
+    tgg:83-84), an empty expert, or an expert index outside [0, E).  The kernel
+    skips them; the result equals the clean queue's, bitwise, in both
+    schedules, and the atomic count is still (queue length) + G."""
+    counts = [300, 0, 129]
+    k, n, bm, bn = 128, 256, 128, 128
+    a, b, offs = make_inputs(counts, k, n, torch.bfloat16, cuda_device)
+    we, wm, wn = orc.build_work_queue(offs.cpu().numpy(), n, bm, bn)
+    bad = [(0, 3, 0), (2, 1, 2), (1, 0, 0), (-1, 0, 0), (3, 0, 1), (0, 0, 5)]
+    rng = np.random.default_rng(4)
+    items = [tuple(t) for t in zip(we.tolist(), wm.tolist(), wn.tolist())] + bad
+    order = rng.permutation(len(items))
+    q = np.array([items[i] for i in order], dtype=np.int32)
+    qe, qm, qn = (torch.from_numpy(np.ascontiguousarray(q[:, j])).to(cuda_device) for j in range(3))
+    m = a.shape[0]
+    ref = None
+    for atomic in (0, 1):
+        c = torch.zeros(m, n, dtype=torch.bfloat16, device=cuda_device)
+        counter = torch.full((1,), 5, dtype=torch.int32, device=cuda_device)
+        nat.check(nat.lib().mgg_grouped_gemm(
+            nat.MGG_DTYPE_BF16, a.data_ptr(), b.data_ptr(), c.data_ptr(), offs.data_ptr(),
+            m, k, n, len(counts), k, k * n, n, n, qe.data_ptr(), qm.data_ptr(), qn.data_ptr(),
+            len(q), bm, bn, 7, atomic, counter.data_ptr() if atomic else None,
+            torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        assert_parity(c, a, b, offs, k)
+        if atomic:
+            assert counter.item() == len(q) + 7
+        if ref is None:
+            ref = c
+        else:
+            assert torch.equal(c, ref)
+
+
 def test_device_queue_builder_bit_exact(cuda_device):
     data = np.load(__import__("pathlib").Path(__file__).parent / "golden" / "queues.npz",
                    allow_pickle=False)
