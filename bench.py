@@ -85,7 +85,7 @@ def event_times_ms(fn, iters, flush=None):
 PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_256x256_bf16_uniform.md"
 
 
-FP8_PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_fp8_256x128_cfg5.md"
+FP8_PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_fp8_cfg5.md"
 
 
 def recorded_traffic(mode, workload, block_m, block_n):
@@ -93,8 +93,8 @@ def recorded_traffic(mode, workload, block_m, block_n):
     (calibrated against a plain copy), when one covers this configuration; else None."""
     if workload == "uniform" and (block_m, block_n) == (256, 256):
         path, key = PROFILE_SUMMARY, f"traffic_bytes_per_launch_{mode}:"
-    elif workload == "fp8" and (block_m, block_n) == (256, 128):
-        path, key = FP8_PROFILE_SUMMARY, f"traffic_bytes_per_launch_fp8_{mode}:"
+    elif workload == "fp8" and (block_m, block_n) in ((256, 128), (192, 128)):
+        path, key = FP8_PROFILE_SUMMARY, f"traffic_bytes_per_launch_fp8_{block_m}x{block_n}_{mode}:"
     else:
         return None
     if not path.exists():
@@ -174,8 +174,9 @@ def fp8_summary(dev, steps: int = 20):
     out = {"config": f"E={case.num_experts}, M={case.m}, K={case.k}, N={case.n}, e4m3 in, bf16 out",
            "algorithmic_bytes": t_bytes, "t_bound_us": round(max(t_flop_bound, t_hbm_bound) * 1e6, 2),
            "runs": {}}
+    out["default_tile"] = f"{gg._default_fp8_block_m(case.m, case.num_experts)}x128"
     best = None
-    for bm, bn in ((256, 128), (128, 128)):
+    for bm, bn in ((256, 128), (192, 128), (128, 128)):
         for mode in ("striped", "atomic"):
             fn = lambda: gg.persistent_grouped_gemm(case.a, b_kn, offs, block_m=bm, block_n=bn,
                                                     use_atomic_queue=mode == "atomic",
@@ -305,13 +306,16 @@ def secondary_main(args, dev):
         flops, nbytes, bound, peak, dtype = case.flops, None, "mfma", PEAK_BF16_TFLOPS, "bf16"
         metric = "expert-MLP forward TFLOP/s (SwiGLU, T=8192 top-2 of 16, H2048 F4096)"
         config_blocks = (256, 256)
+        kernel = "grouped_gemm_kernel<256,256,32,4,8,Bf16,2> (up, SwiGLU) and <256,256,32,4,8,Bf16,0> (down)"
         config = {"workload": f"expert_mlp: T={case.tokens}, top-{case.top_k} of E={case.experts}, "
                               f"H={case.hidden}, F={case.ffn}, SwiGLU", "mode": args.mode}
     else:
         case = workloads.make_fp8_case(device=dev)
         offs = gg.expert_offsets_from_recv_counts(case.counts, device=dev)
         b_kn = case.b_nk.transpose(1, 2)
-        bm, bn = (256, 128) if (args.block_m, args.block_n) == (256, 256) else (args.block_m, args.block_n)
+        # The library's default fp8 tile (192x128 here) unless a tile is named.
+        bm, bn = ((gg._default_fp8_block_m(case.m, case.num_experts), 128)
+                  if (args.block_m, args.block_n) == (256, 256) else (args.block_m, args.block_n))
         step = lambda: gg.persistent_grouped_gemm(case.a, b_kn, offs, num_sms=args.num_sms,
                                                   block_m=bm, block_n=bn,
                                                   use_atomic_queue=args.mode == "atomic",
@@ -321,6 +325,7 @@ def secondary_main(args, dev):
         config = {"workload": f"fp8: E={case.num_experts}, M={case.m}, K={case.k}, N={case.n}",
                   "mode": args.mode, "block_m": bm, "block_n": bn}
         config_blocks = (bm, bn)
+        kernel = f"grouped_gemm_kernel<{bm},{bn},128,{4 if bm == 128 else 3},8,Fp8,0>"
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -352,6 +357,7 @@ def secondary_main(args, dev):
         "roofline": {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
                      "frac": round(achieved / peak, 4),
                      "traffic": recorded_traffic(args.mode, args.workload, *config_blocks),
+                     "kernel": kernel,
                      "algorithmic_flops_per_step": flops, "algorithmic_bytes_per_step": nbytes},
     }), flush=True)
 

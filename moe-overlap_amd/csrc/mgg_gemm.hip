@@ -900,7 +900,9 @@ int launch_typed(int block_m, int block_n, const GemmParams& p, int workers, hip
 }
 
 // fp8: 128-byte rows of K (K-wide 128 stages, two 64-deep MFMA steps), eight
-// waves (two per SIMD) on 256x128 and 128x128 tiles.  A 256x256 tile does not
+// waves (two per SIMD) on 256x128, 192x128 and 128x128 tiles.  192 rows fit
+// experts of 300-400 rows (two tiles, little padding) and give a launch more,
+// smaller tiles to balance over the CUs.  A 256x256 tile does not
 // fit: its 32-byte fp8 fragments, double-buffered, and its accumulators need
 // more than the 256 registers a wave has at two waves per SIMD.
 int launch_fp8(int block_m, int block_n, const GemmParams& p, int workers, hipStream_t stream) {
@@ -911,9 +913,10 @@ int launch_fp8(int block_m, int block_n, const GemmParams& p, int workers, hipSt
     return MGG_OK;                                                                            \
   }
   MGG_CASE(256, 128, 128, 3, MGG_FP8_NW)
+  MGG_CASE(192, 128, 128, 3, MGG_FP8_NW)
   MGG_CASE(128, 128, 128, 4, MGG_FP8_NW)
 #undef MGG_CASE
-  return set_error(MGG_ERR_UNSUPPORTED, "fp8 tiles are 256x128 and 128x128");
+  return set_error(MGG_ERR_UNSUPPORTED, "fp8 tiles are 256x128, 192x128 and 128x128");
 }
 
 template <class T>

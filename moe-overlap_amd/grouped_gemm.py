@@ -332,6 +332,24 @@ def persistent_grouped_gemm(
     return c_op
 
 
+_FP8_BLOCK_M = (256, 192, 128)
+
+
+def _default_fp8_block_m(m_total: int, num_experts: int) -> int:
+    """fp8 tile height by the average rows per expert (top-k routing spreads
+    the counts around it): 128 up to 128 rows, 256 for 129-256 (one tile holds
+    most experts), 192 for 257-384 (two tiles, where 256 would pad to 512),
+    256 above.  Measured on MI355X at E=64, K=2048, N=1408, striped order:
+    averages 96 / 192 / 281 / 384 / 516 / 768 run fastest at 128 / 256 / 192 /
+    192 / 256 (tie with 192) / 256."""
+    avg = -(-m_total // max(num_experts, 1))
+    if avg <= 128:
+        return 128
+    if 256 < avg <= 384:
+        return 192
+    return 256
+
+
 def _persistent_grouped_gemm_fp8(a_cat, b_expert, expert_offsets, a_scale, b_scale, num_sms,
                                  block_m, block_n, use_atomic_queue, work_counter):
     if b_expert.dtype != torch.float8_e4m3fn:
@@ -347,11 +365,10 @@ def _persistent_grouped_gemm_fp8(a_cat, b_expert, expert_offsets, a_scale, b_sca
     device = a_cat.device
     dev_index = device.index if device.index is not None else torch.cuda.current_device()
     if block_m is None or block_n is None:
-        avg = m_total / max(num_experts, 1)
-        block_m = block_m or (256 if avg >= 256 else 128)
+        block_m = block_m or _default_fp8_block_m(m_total, num_experts)
         block_n = block_n or 128
-    if (block_m, block_n) not in ((256, 128), (128, 128)):
-        raise ValueError("fp8 tiles are block_m x block_n = 256x128 or 128x128.")
+    if block_n != 128 or block_m not in _FP8_BLOCK_M:
+        raise ValueError("fp8 tiles are block_m x block_n = 256x128, 192x128 or 128x128.")
     if num_sms is None:
         num_sms = _cu_count(dev_index)
     counter_dev = None

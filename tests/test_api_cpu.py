@@ -72,3 +72,13 @@ def test_queue_cache_hits_and_fifo_eviction():
 def test_flops_helper():
     assert gg.grouped_gemm_flops(torch.tensor([0, 512, 1024]), 2048, 4096) == 2 * 1024 * 2048 * 4096
     assert gg.grouped_gemm_flops([0, 5, 3], 8, 8) == 2 * 5 * 64  # negative counts add nothing
+
+
+@pytest.mark.parametrize("avg,want", [(1, 128), (100, 128), (128, 128), (129, 256), (192, 256),
+                                      (256, 256), (257, 192), (384, 192), (385, 256),
+                                      (512, 256), (4096, 256)])
+def test_default_fp8_tile_height(avg, want):
+    """128 up to 128 rows per expert, 192 for 257-384, else 256; the fp8
+    baseline config (64 experts, 24576 rows: 384 per expert) takes 192."""
+    assert gg._default_fp8_block_m(avg * 64, 64) == want
+    assert gg._default_fp8_block_m(0, 0) == 128

@@ -56,7 +56,7 @@ def assert_close_fp8(c, a, sa, b, sb, offs):
     assert np.all(err <= bound), float((err - bound).max())
 
 
-@pytest.mark.parametrize("block_m,block_n", [(256, 128), (128, 128)])
+@pytest.mark.parametrize("block_m,block_n", [(256, 128), (192, 128), (128, 128)])
 @pytest.mark.parametrize("atomic", [False, True])
 def test_fp8_small_ragged(cuda_device, block_m, block_n, atomic):
     log(f"fp8 small {block_m}x{block_n} atomic={atomic}")
@@ -71,7 +71,7 @@ def test_fp8_small_ragged(cuda_device, block_m, block_n, atomic):
 @pytest.mark.parametrize("seed", range(8))
 def test_fp8_random_shapes(cuda_device, seed):
     """Seeded random fp8 problems: 1-7 experts (some empty or one row), K and N
-    that need padding (K to 16, N to 8) half the time, both tiles, both
+    that need padding (K to 16, N to 8) half the time, the three tiles, both
     schedules, bitwise-equal across schedules."""
     rng = np.random.default_rng(1000 + seed)
     e = int(rng.integers(1, 8))
@@ -80,7 +80,7 @@ def test_fp8_random_shapes(cuda_device, seed):
     counts[rng.random(e) < 0.15] = 1
     k = int(rng.integers(1, 90)) * (16 if seed % 2 == 0 else 7)
     n = int(rng.integers(1, 60)) * (8 if seed % 2 == 0 else 5)
-    bm = (256, 128)[seed % 2]
+    bm = (256, 192, 128)[seed % 3]
     log(f"fp8 random seed={seed} counts={counts.tolist()} K={k} N={n} block_m={bm}")
     a, sa, b, sb, offs = fp8_inputs(counts.tolist(), k, n, seed=seed, device=cuda_device)
     outs = [gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, block_m=bm, block_n=128,
@@ -112,7 +112,7 @@ def test_fp8_work_counter_and_errors(cuda_device):
     assert int(wc.item()) == 2 * 3 * 2 + 7  # W = sum ceil(300/128) * ceil(256/128)
     with pytest.raises(ValueError, match="a_scale"):
         gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs)
-    with pytest.raises(ValueError, match="256x128 or 128x128"):
+    with pytest.raises(ValueError, match="256x128, 192x128 or 128x128"):
         gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, block_m=64, block_n=64,
                                    a_scale=sa, b_scale=sb)
 
@@ -120,12 +120,20 @@ def test_fp8_work_counter_and_errors(cuda_device):
 def test_fp8_baseline_config(cuda_device):
     """BASELINE fp8 config: E=64, M=24576 (top-6 of 4096 tokens), K=2048,
     N=1408; against the decoded-fp8 fp32 product per expert on the GPU and
-    against the unquantised fp32 GEMM (north_star: relative error <= 5e-2)."""
+    against the unquantised fp32 GEMM (north_star: relative error <= 5e-2).
+    The default tile here is 192x128; 256x128 and 128x128 must give the same
+    bits (each output's K sum runs in the same order whatever the tile height)."""
     log("fp8 cfg5")
     case = workloads.make_fp8_case(device=cuda_device, keep_reference=True)
     offs = gg.expert_offsets_from_recv_counts(case.counts, device=cuda_device)
+    assert gg._default_fp8_block_m(case.m, case.num_experts) == 192
     c = gg.persistent_grouped_gemm(case.a, case.b_nk.transpose(1, 2), offs,
-                                   a_scale=case.a_scale, b_scale=case.b_scale).float()
+                                   a_scale=case.a_scale, b_scale=case.b_scale)
+    for bm in (256, 128):
+        other = gg.persistent_grouped_gemm(case.a, case.b_nk.transpose(1, 2), offs, block_m=bm,
+                                           block_n=128, a_scale=case.a_scale, b_scale=case.b_scale)
+        assert torch.equal(c, other), bm
+    c = c.float()
     o = offs.cpu().tolist()
     num = den = unq_num = 0.0
     worst = 0.0
