@@ -200,6 +200,13 @@ __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t soff, 
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
+// One 4-byte-per-lane DMA: lane l's word lands at LDS byte address lds + 4*l.
+__device__ __forceinline__ void dma4(i32x4 rsrc, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(lds)
+               : "memory", "m0");
+}
 // Waits until at most N of this wave's DMAs are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_dma() {
@@ -384,10 +391,18 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   const uint8_t* a_bytes = reinterpret_cast<const uint8_t*>(p.a);
   const uint8_t* b_bytes = reinterpret_cast<const uint8_t*>(p.b);
 
-  // The DMA state of the tile whose stages are being issued.
+  // The DMA state of the tile whose stages are being issued (and, for scaled
+  // types, its coordinates and the LDS buffer its scales go to).
   i32x4 a_rsrc, b_rsrc;
   uint32_t b_voff[kBPerWave];
-  auto set_sources = [&](const Coords& c) {
+  Coords iss{};
+  int iss_scale_buf = 0;
+  // Scale buffer of the tile being multiplied: it alternates per tile, so the
+  // next tile's scales can arrive while this tile's epilogue reads its own.
+  int scale_buf = 0;
+  auto set_sources = [&](const Coords& c, int scale_slot) {
+    iss = c;
+    iss_scale_buf = scale_slot;
     int64_t r0 = c.row_base;
     r0 = r0 < 0 ? 0 : (r0 > p.m ? p.m : r0);
     const int64_t r_end = c.row_base + c.rows_valid < p.m ? c.row_base + c.rows_valid : p.m;
@@ -454,7 +469,34 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
       }
     }
   };
-  auto issue_stage = [&](int s) { issue_part(s, 0, kDmaPerStage); };
+  // Scaled types: the tile's BM row scales and BN column scales go to its LDS
+  // scale buffer by DMA with its stage 0 (one 64-word DMA per wave for the
+  // first (BM+BN)/64 waves), so the first stage wait covers them; rows past
+  // the tile's valid rows and columns past N read as zeros (descriptor ends).
+  auto issue_scales = [&]() {
+    if constexpr (T::kScaled) {
+      static_assert(BM % 64 == 0 && BN % 64 == 0 && (BM + BN) / 64 <= NW, "one scale DMA per wave");
+      if ((int)wave < (BM + BN) / 64) {
+        const uint32_t dst = lds_addr(s_scale + iss_scale_buf * (BM + BN) + 64 * wave);
+        if (64 * (int)wave < BM) {
+          int64_t rows = p.m - iss.row_base;
+          rows = rows < iss.rows_valid ? rows : iss.rows_valid;
+          const i32x4 rs = make_rsrc4(p.a_scale + (iss.row_base > 0 ? iss.row_base : 0),
+                                      iss.row_base >= 0 && rows > 0 ? rows * 4 : 0);
+          dma4(rs, (uint32_t)(64 * wave + lane) * 4, dst);
+        } else {
+          int64_t cols = p.n - iss.n0;
+          cols = cols < BN ? cols : BN;
+          const i32x4 rs = make_rsrc4(p.b_scale + (int64_t)iss.e * p.n + iss.n0, cols > 0 ? cols * 4 : 0);
+          dma4(rs, (uint32_t)(64 * wave - BM + lane) * 4, dst);
+        }
+      }
+    }
+  };
+  auto issue_stage = [&](int s) {
+    issue_part(s, 0, kDmaPerStage);
+    if (s == 0) issue_scales();
+  };
 
   // ---- fragment addresses (LDS bytes, stage 0) ----------------------------
   const int frag_row = lane & 31;
@@ -615,25 +657,10 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     for (int g = 0; g < 4; ++g) mfma_group((p0 + kSteps - 1) & 1, g);
   };
   // All stages of the current tile; stages 0 .. min(kStages-1, nk)-1 have
-  // been issued.  Returns after the last stage's fragments have been read
-  // and its MFMAs issued.
-  // Scaled types: the tile's row and column scales go to LDS (buffer `sb`
-  // alternates per tile, so the previous tile's epilogue may still read the
-  // other one) before the first barrier of the tile.
-  int scale_buf = 0;
-  auto main_loop = [&](const Coords& c, bool take_ticket, int32_t& ticket) {
-    if constexpr (T::kScaled) {
-      float* sc = s_scale + scale_buf * (BM + BN);
-      for (int i = tid; i < BM + BN; i += NW * 64) {
-        float v = 0.0f;
-        if (i < BM) {
-          if (i < c.rows_valid) v = p.a_scale[c.row_base + i];
-        } else if (c.n0 + (i - BM) < p.n) {
-          v = p.b_scale[(int64_t)c.e * p.n + c.n0 + (i - BM)];
-        }
-        sc[i] = v;
-      }
-    }
+  // been issued (with a scaled type's scales, in LDS scale buffer scale_buf).
+  // Returns after the last stage's fragments have been read and its MFMAs
+  // issued.
+  auto main_loop = [&](bool take_ticket, int32_t& ticket) {
 #pragma unroll
     for (int i = 0; i < kNB; ++i)
 #pragma unroll
@@ -758,13 +785,13 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   Coords cur;
   int32_t w = find_valid(first, cur);
   if ((uint32_t)w >= (uint32_t)W) return;
-  set_sources(cur);
+  set_sources(cur, scale_buf);
 #pragma unroll
   for (int s = 0; s < kStages - 1; ++s)
     if (s < nk) issue_stage(issued = s);
   for (;;) {
     int32_t ticket = 0;
-    main_loop(cur, p.atomic != 0, ticket);
+    main_loop(p.atomic != 0, ticket);
     // The next item: the ticket taken during this tile, or the next stripe.
     if (p.atomic && tid == 0) *s_item = ticket;
     __syncthreads();  // every wave is done reading this tile's LDS stages; s_item is visible
@@ -777,7 +804,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     // DMAs issued after the stage it waits for.
     issued = -1;
     if (more) {
-      set_sources(nxt);
+      set_sources(nxt, scale_buf ^ 1);
       if (nk > 0) issue_stage(issued = 0);
     }
     epilogue(cur);
