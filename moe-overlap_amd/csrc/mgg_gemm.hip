@@ -30,6 +30,14 @@
 #ifndef MGG_NW256
 #define MGG_NW256 8
 #endif
+// A in 64-deep blocks on the 256x256 16-bit tile (see ablk_mode), with a B
+// ring of MGG_ABLK_BS 32-deep stages.
+#ifndef MGG_ABLK
+#define MGG_ABLK 1
+#endif
+#ifndef MGG_ABLK_BS
+#define MGG_ABLK_BS 4
+#endif
 #ifndef MGG_FP8_NW
 #define MGG_FP8_NW 8
 #endif
@@ -243,6 +251,16 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
+// A in blocks of two stages: the 256x256 16-bit N-major tile with 32-deep
+// stages loads A in 64-deep blocks, so each A row segment is a full 128-byte
+// line (half the L2 requests of 64-byte segments), into two LDS slots of
+// 32 KiB, while B keeps 32-deep stages in a ring of MGG_ABLK_BS slots.
+template <int BM, int BN, int SBK, int NSTAGE, int NW, class T>
+constexpr bool ablk_mode() {
+  return MGG_ABLK && BM == 256 && BN == 256 && SBK == 32 && NSTAGE == 4 && NW == 8 &&
+         T::kElem == 2 && !T::kBKMajor && !T::kScaled;
+}
+
 // One workgroup's share of the queue: a persistent loop over tiles.  All
 // arguments, and every branch below that guards a barrier, are uniform across
 // the workgroup.
@@ -288,8 +306,19 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   // LDS rows of B: K-major B is stored like A (BN rows of the stage's K
   // bytes); otherwise K rows of BN 16-bit values.
   constexpr int kBRowBytes = T::kBKMajor ? kARowBytes : BN * 2;
-  constexpr int kAPerWave = BM / (NW * kARowsPerDma);  // A DMAs per wave per stage
-  constexpr int kBPerWave = kBStage / (1024 * NW);     // B DMAs per wave per stage
+  // LDS layout of A: a stage per slot, or (kABlk) a block of two stages per
+  // slot with 128-byte rows; kAPerWave counts the DMAs of one slot.
+  constexpr bool kABlk = ablk_mode<BM, BN, SBK, NSTAGE, NW, T>();
+  constexpr int kALdsRow = kABlk ? 2 * kARowBytes : kARowBytes;
+  constexpr int kALdsChunks = kALdsRow / 16;
+  constexpr int kARowsPerDmaL = 64 / kALdsChunks;
+  constexpr int kASlot = BM * kALdsRow;
+  constexpr int kASlots = kABlk ? 2 : kStages;
+  constexpr int kBSlots = kABlk ? MGG_ABLK_BS : kStages;
+  constexpr int kLB = kBSlots - 1;  // kABlk: B stages issued ahead
+  static_assert(!kABlk || (kLB >= 3 && kSteps == 2), "A blocks need a B ring of 4+ and 2-step stages");
+  constexpr int kAPerWave = BM / (NW * kARowsPerDmaL);  // A DMAs per wave per A slot
+  constexpr int kBPerWave = kBStage / (1024 * NW);      // B DMAs per wave per stage
   constexpr int kWN = NW / 2;                          // waves along N (2 along M)
   static_assert(kAPerWave >= 1 && kBPerWave >= 1, "tile too small for the wave count");
   static_assert(kSteps == 1 || kSteps == 2 || kSteps == 4, "a stage must be 1, 2 or 4 MFMA K steps");
@@ -374,11 +403,11 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   // are 32-bit (the host bounds lda and ldb_k).  ldb_k is the stride between
   // B's rows: K rows for N-major B, N rows for K-major B.
   auto a_swz = [](int r) {
-    return kAChunks == 2 ? (r >> 3) & 1 : kAChunks == 4 ? (r >> 2) & 3 : (r >> 1) & 7;
+    return kALdsChunks == 2 ? (r >> 3) & 1 : kALdsChunks == 4 ? (r >> 2) & 3 : (r >> 1) & 7;
   };
-  // Chunk (row, K position) moved by lane `lane` in the t-th DMA of a stage.
-  auto a_row = [&](int t) { return kARowsPerDma * (wave * kAPerWave + t) + lane / kAChunks; };
-  auto a_kpos = [&](int t) { return kChunkElems * ((lane % kAChunks) ^ a_swz(a_row(t))); };
+  // Chunk (row, K position) moved by lane `lane` in the t-th DMA of an A slot.
+  auto a_row = [&](int t) { return kARowsPerDmaL * (wave * kAPerWave + t) + lane / kALdsChunks; };
+  auto a_kpos = [&](int t) { return kChunkElems * ((lane % kALdsChunks) ^ a_swz(a_row(t))); };
   auto b_krow = [&](int t) { return (wave * kBPerWave + t) * kBRowsPerDma + lane / kBChunks; };
   // K-major B: row n of the tile and the K position of the chunk.
   auto b_kpos = [&](int t) { return kChunkElems * ((lane % kBChunks) ^ a_swz(b_krow(t))); };
@@ -387,7 +416,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   for (int t = 0; t < kAPerWave; ++t) a_voff[t] = (uint32_t)((a_row(t) * p.lda + a_kpos(t)) * kE);
   const uint32_t b_row_bytes = (uint32_t)(p.ldb_k * kE);
   const uint32_t lds_a0 = lds_addr(lds);
-  const uint32_t lds_b0 = lds_a0 + kStages * kAStage;
+  const uint32_t lds_b0 = lds_a0 + kASlots * kASlot;
   const uint8_t* a_bytes = reinterpret_cast<const uint8_t*>(p.a);
   const uint8_t* b_bytes = reinterpret_cast<const uint8_t*>(p.b);
 
@@ -503,14 +532,18 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   const int half = lane >> 5;
   // A fragment of K step kk: chunks kk*kStepChunks + half*kFragChunks + q of
   // row frag_row (+32j rows per block, the same swizzle).
-  const uint32_t a_frag0 = (uint32_t)((wm * (BM / 2) + frag_row) * kARowBytes);
-  uint32_t a_off[kSteps][kFragChunks];
+  const uint32_t a_frag0 = (uint32_t)((wm * (BM / 2) + frag_row) * kALdsRow);
+  // [half of an A block (kABlk; else 0)][K step][chunk]
+  uint32_t a_off[kABlk ? 2 : 1][kSteps][kFragChunks];
 #pragma unroll
-  for (int kk = 0; kk < kSteps; ++kk)
+  for (int h = 0; h < (kABlk ? 2 : 1); ++h)
 #pragma unroll
-    for (int q = 0; q < kFragChunks; ++q)
-      a_off[kk][q] = lds_a0 + a_frag0 +
-                     (uint32_t)(((kk * kStepChunks + half * kFragChunks + q) ^ a_swz(frag_row)) * 16);
+    for (int kk = 0; kk < kSteps; ++kk)
+#pragma unroll
+      for (int q = 0; q < kFragChunks; ++q)
+        a_off[h][kk][q] =
+            lds_a0 + a_frag0 +
+            (uint32_t)((((h * kSteps + kk) * kStepChunks + half * kFragChunks + q) ^ a_swz(frag_row)) * 16);
   const int tg = lane >> 4, ts = lane & 15;  // transposing-read group and source lane
   const int b_row_l = 8 * (tg >> 1) + (ts >> 2);
   const int b_swz = BN >= 128 ? 4 * ((ts >> 2) & 3) : 4 * ((ts >> 3) & 1);
@@ -547,7 +580,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     return v;
   };
   auto read_a = [&](int f, int buf, int kk, int j) {
-    fa[f][j] = read_rows(a_off[kk], buf * kAStage + 32 * kARowBytes * j);
+    fa[f][j] = read_rows(a_off[0][kk], buf * kASlot + 32 * kALdsRow * j);
   };
   auto read_b = [&](int f, int buf, int kk, int i) {
     if constexpr (T::kBKMajor) {
@@ -660,6 +693,103 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   // been issued (with a scaled type's scales, in LDS scale buffer scale_buf).
   // Returns after the last stage's fragments have been read and its MFMAs
   // issued.
+  // ---- A in blocks of two stages (kABlk) -----------------------------------
+  // Stage s multiplies A block s/2 (LDS slot (s/2)&1, K half s&1) and B stage s
+  // (slot s % kBSlots).  Stage s issues, when s is even, A block s/2+1 (into
+  // the slot block s/2-1 left; its four DMAs first), then B stage s+kLB (into
+  // the slot stage s-1 left).  Loads past K are issued all the same (zeros,
+  // no memory reads: offsets past the descriptors), so every wait counts a
+  // fixed number of later DMAs: 4 after a stage of odd index (the A block of
+  // the next stage is the last load it needs), 8 (kLB 3) or 10 (kLB >= 4)
+  // after one of even index, 2*(kLB-1) at a tile's start.
+  constexpr int kWaitOdd = 2 * kBPerWave;
+  // Even kt, kLB 3: the last load stage kt+1 needs is B stage kt+1 (issued in
+  // stage kt-2 after that stage's A block); after it come stage kt-1's B and
+  // stage kt's A block and B.  kLB >= 4: it is A block kt/2 (issued first in
+  // stage kt-2); after it come stage kt-2's B, stage kt-1's B and stage kt's
+  // A block and B.
+  constexpr int kWaitEven = kLB == 3 ? kBPerWave + kAPerWave + kBPerWave
+                                     : kBPerWave + kBPerWave + kAPerWave + kBPerWave;
+  static_assert(!kABlk || (kAPerWave == 4 && kBPerWave == 2), "A-block DMA shares assume 4 + 2");
+  auto issue_ablock = [&](int m, int t0, int t1) {  // DMAs [t0, t1) of A block m
+    const int k0 = m * 2 * kBK;
+    const uint32_t la = lds_a0 + (m & 1) * kASlot + wave * kAPerWave * 1024;
+    const bool full = k0 + 2 * kBK <= k_size;
+#pragma unroll
+    for (int t = t0; t < t1; ++t) {
+      if (full) {
+        dma16(a_rsrc, a_voff[t], (uint32_t)k0 * kE, la + t * 1024);
+      } else {
+        const uint32_t v = k0 + a_kpos(t) < k_size ? a_voff[t] + (uint32_t)k0 * kE : kOutOfRange;
+        dma16(a_rsrc, v, 0u, la + t * 1024);
+      }
+    }
+  };
+  auto issue_bstage = [&](int st, int d0, int d1) {  // DMAs [d0, d1) of B stage st
+    const int k0 = st * kBK;
+    const uint32_t lb = lds_b0 + (st % kBSlots) * kBStage + wave * kBPerWave * 1024;
+    const bool full = k0 + kBK <= k_size;
+#pragma unroll
+    for (int t = d0; t < d1; ++t) {
+      if (full) {
+        dma16(b_rsrc, b_voff[t], (uint32_t)k0 * b_row_bytes, lb + t * 1024);
+      } else {
+        const uint32_t v =
+            k0 + b_krow(t) < k_size ? b_voff[t] + (uint32_t)k0 * b_row_bytes : kOutOfRange;
+        dma16(b_rsrc, v, 0u, lb + t * 1024);
+      }
+    }
+  };
+  // Half `part` of the fragments of K step kk of stage st (A half H of its block).
+  auto read_kstep_ab = [&](auto H, int f, int st, int kk, int part) {
+    constexpr int h = decltype(H)::value;
+    const int aslot = (st >> 1) & 1;
+#pragma unroll
+    for (int j = part * kMB / 2; j < (part + 1) * kMB / 2; ++j)
+      fa[f][j] = read_rows(a_off[kABlk ? h : 0][kk], aslot * kASlot + 32 * kALdsRow * j);
+#pragma unroll
+    for (int i = part * kNB / 2; i < (part + 1) * kNB / 2 + (kNB == 1 && part == 0); ++i)
+      read_b(f, st % kBSlots, kk, i);
+  };
+  // Stage kt of A half H (kt % 2 == H), in run_worker's stage order: K step 0
+  // on fragment buffer 0 while step 1's fragments are read and this stage's
+  // DMAs go out, then step 1, the wait and barrier for stage kt+1, and its
+  // first fragments.
+  auto stage_ab = [&](auto H, int kt) {
+    constexpr int h = decltype(H)::value;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      mfma_group(0, g);
+      if (g < 2) read_kstep_ab(H, 1, kt, 1, g);
+      if constexpr (h == 0) {
+        if (g < 2) issue_ablock(kt / 2 + 1, 2 * g, 2 * g + 2);
+        else issue_bstage(kt + kLB, g - 2, g - 1);
+      } else {
+        if (g == 0 || g == 2) issue_bstage(kt + kLB, g / 2, g / 2 + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    mfma_group(1, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_dma<h == 0 ? kWaitEven : kWaitOdd>();
+    __syncthreads();
+    mfma_group(1, 1);
+    read_kstep_ab(IntConst<1 - h>{}, 0, kt + 1, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_group(1, 2);
+    read_kstep_ab(IntConst<1 - h>{}, 0, kt + 1, 0, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_group(1, 3);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // A tile's first loads: A block 0, then B stages 0 .. kLB-1.
+  auto prologue_ab = [&](bool first_only) {
+    issue_ablock(0, 0, kAPerWave);
+    issue_bstage(0, 0, kBPerWave);
+    if (!first_only)
+      for (int st = 1; st < kLB; ++st) issue_bstage(st, 0, kBPerWave);
+  };
+
   auto main_loop = [&](bool take_ticket, int32_t& ticket) {
 #pragma unroll
     for (int i = 0; i < kNB; ++i)
@@ -667,11 +797,24 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
       for (int j = 0; j < kMB; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    wait_stage(0, issued);
+    if constexpr (kABlk)
+      wait_dma<2 * (kLB - 1) * kBPerWave / 2>();
+    else
+      wait_stage(0, issued);
     __syncthreads();
     // The next tile's ticket, taken after the first wait so that this
     // wave's first DMA wait does not also wait for the atomic.
     if (take_ticket && tid == 0) ticket = G + atomicAdd(p.counter, 1);
+    if constexpr (kABlk) {
+      read_kstep_ab(IntConst<0>{}, 0, 0, 0, 0);
+      read_kstep_ab(IntConst<0>{}, 0, 0, 0, 1);
+      const int nk2 = (nk + 1) & ~1;  // pairs of stages; an odd count ends on a zero stage
+      for (int kt = 0; kt < nk2; kt += 2) {
+        stage_ab(IntConst<0>{}, kt);
+        stage_ab(IntConst<1>{}, kt + 1);
+      }
+      return;
+    }
     if (nk > 0) {
       read_kstep(0, 0, 0, 0);
       read_kstep(0, 0, 0, 1);
@@ -786,9 +929,13 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   int32_t w = find_valid(first, cur);
   if ((uint32_t)w >= (uint32_t)W) return;
   set_sources(cur, scale_buf);
+  if constexpr (kABlk) {
+    prologue_ab(false);
+  } else {
 #pragma unroll
-  for (int s = 0; s < kStages - 1; ++s)
-    if (s < nk) issue_stage(issued = s);
+    for (int s = 0; s < kStages - 1; ++s)
+      if (s < nk) issue_stage(issued = s);
+  }
   for (;;) {
     int32_t ticket = 0;
     main_loop(p.atomic != 0, ticket);
@@ -805,28 +952,37 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     issued = -1;
     if (more) {
       set_sources(nxt, scale_buf ^ 1);
-      if (nk > 0) issue_stage(issued = 0);
+      if constexpr (kABlk)
+        prologue_ab(true);
+      else if (nk > 0)
+        issue_stage(issued = 0);
     }
     epilogue(cur);
     if (!more) break;
+    if constexpr (kABlk) {
+      for (int st = 1; st < kLB; ++st) issue_bstage(st, 0, kBPerWave);
+    } else {
 #pragma unroll
-    for (int s = 1; s < kStages - 1; ++s)
-      if (s < nk) issue_stage(issued = s);
+      for (int s = 1; s < kStages - 1; ++s)
+        if (s < nk) issue_stage(issued = s);
+    }
     cur = nxt;
     w = next;
     scale_buf ^= 1;
   }
 }
 
-template <int BM, int BN, int SBK, int NSTAGE, class T>
+template <int BM, int BN, int SBK, int NSTAGE, class T, int NW = 8>
 constexpr int lds_bytes() {
+  if constexpr (ablk_mode<BM, BN, SBK, NSTAGE, NW, T>())
+    return 2 * BM * 2 * SBK * T::kElem + MGG_ABLK_BS * SBK * BN * T::kElem;
   return NSTAGE * (BM + BN) * SBK * T::kElem;
 }
 // Row offsets of the derived queue's experts are kept in LDS when they fit
 // beside the stages (otherwise each tile reads them from global memory).
 template <int BM, int BN, int SBK, int NSTAGE, int NT, class T>
 constexpr bool offsets_in_lds() {
-  return lds_bytes<BM, BN, SBK, NSTAGE, T>() + 2 * 4 * (kMaxLdsExpertsGemm + 1) + 4 * NT + 256 +
+  return lds_bytes<BM, BN, SBK, NSTAGE, T, NT / 64>() + 2 * 4 * (kMaxLdsExpertsGemm + 1) + 4 * NT + 256 +
              (T::kScaled ? 8 * (BM + BN) : 0) <=
          160 * 1024;
 }
@@ -838,10 +994,10 @@ template <int BM, int BN, int SBK, int NSTAGE, int NW, class T, int EPI>
 __global__ __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64),
                           amdgpu_waves_per_eu(NW / 4, NW / 4))) void
 grouped_gemm_kernel(GemmParams p) {
-  static_assert(lds_bytes<BM, BN, SBK, NSTAGE, T>() <= 144 * 1024, "LDS stages exceed the budget");
+  static_assert(lds_bytes<BM, BN, SBK, NSTAGE, T, NW>() <= 144 * 1024, "LDS stages exceed the budget");
   constexpr int NT = NW * 64;
   constexpr bool kOffsLds = offsets_in_lds<BM, BN, SBK, NSTAGE, NT, T>();
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes<BM, BN, SBK, NSTAGE, T>()];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes<BM, BN, SBK, NSTAGE, T, NW>()];
   __shared__ int32_t s_prefix[kMaxLdsExpertsGemm + 1];
   __shared__ int32_t s_offs[kOffsLds ? kMaxLdsExpertsGemm + 1 : 1];
   __shared__ int32_t s_scan[NT];
