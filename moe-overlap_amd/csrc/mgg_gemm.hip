@@ -701,7 +701,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   // no memory reads: offsets past the descriptors), so every wait counts a
   // fixed number of later DMAs: 4 after a stage of odd index (the A block of
   // the next stage is the last load it needs), 8 (kLB 3) or 10 (kLB >= 4)
-  // after one of even index, 2*(kLB-1) at a tile's start.
+  // after one of even index, (kLB-1) B stages' worth at a tile's start.
   constexpr int kWaitOdd = 2 * kBPerWave;
   // Even kt, kLB 3: the last load stage kt+1 needs is B stage kt+1 (issued in
   // stage kt-2 after that stage's A block); after it come stage kt-1's B and
@@ -798,7 +798,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     if constexpr (kABlk)
-      wait_dma<2 * (kLB - 1) * kBPerWave / 2>();
+      wait_dma<(kLB - 1) * kBPerWave>();  // B stages 1 .. kLB-1 issued after stage 0's B
     else
       wait_stage(0, issued);
     __syncthreads();
