@@ -104,6 +104,30 @@ def test_small_ragged_parity_all_modes(cuda_device, case, dtype):
                 assert torch.equal(got, ref), (blocks, atomic, queue)
 
 
+# K values around the 256x256 tile's staging: A moves in 64-deep blocks and B
+# in 32-deep stages, so K = 8 and 40 end inside a B stage, 32 and 96 give an
+# odd stage count (half an A block at the end), 64 and 128 whole blocks, 72 and
+# 136 one stage past a block, 2056 a long loop with a tail.
+ABLOCK_KS = [8, 32, 40, 64, 72, 96, 128, 136, 2056]
+
+
+@pytest.mark.parametrize("k", ABLOCK_KS)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_k_staging_edges_256x256(cuda_device, k, dtype):
+    counts = [300, 0, 257, 1, 512]
+    n = 264
+    a, b, offs = make_inputs(counts, k, n, dtype, cuda_device, seed=k, extra_rows=5)
+    outs = []
+    for atomic in (False, True):
+        log(f"k={k} dtype={dtype} atomic={atomic}")
+        c = gg.persistent_grouped_gemm(a, b, offs, block_m=256, block_n=256, use_atomic_queue=atomic)
+        torch.cuda.synchronize()
+        assert_parity(c, a, b, offs, k)
+        outs.append(c)
+    mask = torch.from_numpy(covered_rows(offs)).to(cuda_device)
+    assert torch.equal(outs[0][: mask.numel()][mask], outs[1][: mask.numel()][mask])
+
+
 def random_case(seed):
     """A seeded random problem: 1-9 experts with counts in [0, 600] (some
     empty, some a single row), K in [8, 1200] and N in [8, 700] (multiples of
