@@ -465,6 +465,17 @@ def main():
         tl = event_times_ms(loop, 5)
         extra["torch_loop_gpu_ms_median"] = round(median(tl), 4)
         extra["torch_loop_gpu_tflops"] = round(flops / (median(tl) * 1e-3) / 1e12, 1)
+        counts_l = case.counts.tolist()
+        if len(set(counts_l)) == 1 and counts_l[0] > 0:
+            # Equal counts make the problem one batched GEMM: the vendor library's batched
+            # kernel (torch.bmm -> hipBLASLt) on the same operands, for reference.
+            e, c = len(counts_l), counts_l[0]
+            a3 = case.a[: e * c].view(e, c, case.k)
+            bmm = lambda: torch.bmm(a3, case.b)
+            event_times_ms(bmm, 50)
+            tb = event_times_ms(bmm, 40)
+            extra["hipblaslt_bmm_ms_median"] = round(median(tb), 4)
+            extra["hipblaslt_bmm_tflops"] = round(flops / (median(tb) * 1e-3) / 1e12, 1)
         extra["overlap"] = overlap_summary(case, offs, dev)
         # Cache-cold launches: a 512 MiB write evicts L2 and the 256 MB MALL.
         scratch = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
