@@ -864,33 +864,67 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     // col already includes 8*half
     if (row_ok && col < cols) *reinterpret_cast<u32x4*>(crow + col) = v;
   };
-  // Stores through LDS (the A-block tile, no SwiGLU): a wave's columns of a
-  // row are one 128-byte line of C, but a store instruction straight from the
-  // MFMA layout writes 32 rows x 32 bytes.  Each 32-row block instead goes to
-  // a 4 KiB LDS region of the wave (row r, 16-byte chunk ch at ch ^ ((r>>1)&7),
-  // conflict-free both ways) and comes back as 8 rows x 8 chunks per
-  // instruction, so every store covers 8 full lines (a 32 MiB burst of such
-  // stores measured 30% faster).  The regions tile A slot 1: no DMA is in
-  // flight into it (the last stage's wait retired the zero-fill block the
-  // last even stage sent there) and the next tile first fills it in its first
-  // stage, after the barrier that opens its K loop.
+  // Stores through LDS: a wave's output columns of a row are one 64- or
+  // 128-byte segment of C, but a store instruction straight from the MFMA
+  // layout writes 32 rows x 32 bytes.  Each 32-row block instead goes to an
+  // LDS region of the wave (row r, 16-byte chunk ch at ch ^ swz(r),
+  // conflict-free both ways) and comes back as whole row segments, 8 rows of
+  // 128 bytes or 16 of 64 per instruction (32 MiB bursts of such stores
+  // measured 30% faster than 32-byte segments; 64-byte ones 19% faster).
+  // The region is free for the whole epilogue:
+  // * A-block tile: a 4 KiB share of A slot 1.  No DMA is in flight into it
+  //   (the last stage's wait retired the zero-fill block the last even stage
+  //   sent there) and the next tile first fills it in its first stage, after
+  //   the barrier that opens its K loop.
+  // * Other tiles: the wave's own share of buffer 1's A stage.  Every DMA has
+  //   retired before the last stage (its wait is for all of them), and only
+  //   this wave writes that share, with the next tile's stage 1, issued after
+  //   this wave's epilogue.
   // The LDS addresses are derived from an opaque copy of the lane index taken
   // in the epilogue: otherwise the compiler computes them once per kernel and
   // keeps them live through the K loop, which then spills.
-  constexpr bool kLineStores = kABlk && EPI != kEpiSwiglu && BN / kWN == 64 && NW * 4096 <= kASlot;
-  const uint32_t line_region = (uint32_t)kASlot + wave * 4096u;
+  constexpr int kOutCols = EPI == kEpiSwiglu ? BN / kWN / 2 : BN / kWN;  // per wave and row
+  constexpr int kLineChunks = kOutCols * 2 / 16;  // 16-byte chunks of a wave's row segment
+  constexpr bool kLineStores =
+      (kLineChunks == 4 || kLineChunks == 8) &&
+      (kABlk ? NW * 4096 <= kASlot : kStages >= 2 && kAPerWave * 1024 >= 32 * 16 * kLineChunks);
+  const uint32_t line_region =
+      kABlk ? (uint32_t)kASlot + wave * 4096u : (uint32_t)kAStage + wave * (uint32_t)kAPerWave * 1024u;
   auto opaque_lane = [&]() {
     int l = lane;
     asm volatile("" : "+v"(l));
     return l;
   };
-  auto line_put = [&](int r, int ch, const u32x4& v) {
-    *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(
-        lds_ptr(lds) + line_region + r * 128 + ((ch ^ ((r >> 1) & 7)) * 16)) = v;
+  auto line_addr = [&](int r, int ch) {
+    const int swz = kLineChunks == 8 ? (r >> 1) & 7 : (r >> 2) & 3;
+    return line_region + (uint32_t)(r * 16 * kLineChunks + ((ch ^ swz) * 16));
   };
-  auto line_get = [&](int r, int ch) -> u32x4 {
-    return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
-        lds_ptr(lds) + line_region + r * 128 + ((ch ^ ((r >> 1) & 7)) * 16));
+  auto line_put = [&](int r, int ch, const u32x4& v) {
+    *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(lds_ptr(lds) + line_addr(r, ch)) = v;
+  };
+  // Row block j (32 rows) of this wave, all in LDS: store its row segments.
+  // col0: C column of the wave's first output column; cols: C's columns.
+  auto line_flush = [&](const Coords& c, int j, int ol, int64_t col0, int64_t cols) {
+    // Lanes read what other lanes wrote: keep the compiler from moving LDS
+    // accesses across this point (the hardware runs a wave's LDS operations
+    // in order), here and after the reads.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    constexpr int kRowsPer = 64 / kLineChunks;  // rows per store instruction
+    const int ch = ol % kLineChunks;
+    const int64_t col = col0 + 8 * ch;
+#pragma unroll
+    for (int q = 0; q < 32 / kRowsPer; ++q) {
+      const int rr = kRowsPer * q + ol / kLineChunks;
+      const u32x4 v =
+          *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(lds_ptr(lds) + line_addr(rr, ch));
+      const int mr = wm * (BM / 2) + 32 * j + rr;
+      const int64_t gr = c.row_base + mr;
+      if (mr < c.rows_valid && gr >= 0 && gr <= last_row && col < cols)
+        *reinterpret_cast<u32x4*>(p.c + gr * p.ldc + col) = v;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
   };
   auto epilogue = [&](const Coords& c) {
     const float* sc = s_scale + scale_buf * (BM + BN);
@@ -901,6 +935,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
       const int64_t grow = c.row_base + m;
       const bool row_ok = m < c.rows_valid && grow >= 0 && grow <= last_row;
       uint16_t* crow = p.c + grow * p.ldc;
+      const int ol = kLineStores ? opaque_lane() : lane;
       if constexpr (EPI == kEpiSwiglu) {
 #pragma unroll
         for (int ip = 0; ip < kNB / 2; ++ip) {
@@ -913,11 +948,14 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
               y0[q] = silu_mul(acc[2 * ip][j][8 * pp + q], acc[2 * ip + 1][j][8 * pp + q]);
               y1[q] = silu_mul(acc[2 * ip][j][8 * pp + 4 + q], acc[2 * ip + 1][j][8 * pp + 4 + q]);
             }
-            store_pair(crow, f0 + 16 * pp + 8 * half, p.n / 2, row_ok, y0, y1);
+            if constexpr (kLineStores)
+              line_put(ol & 31, 4 * ip + 2 * pp + (ol >> 5), pack_pair(y0, y1));
+            else
+              store_pair(crow, f0 + 16 * pp + 8 * half, p.n / 2, row_ok, y0, y1);
           }
         }
+        if constexpr (kLineStores) line_flush(c, j, ol, (c.n0 + wn * (BN / kWN)) / 2, p.n / 2);
       } else {
-        const int ol = kLineStores ? opaque_lane() : lane;
 #pragma unroll
         for (int i = 0; i < kNB; ++i) {
           const int cb = wn * (BN / kWN) + 32 * i;  // tile column of the block
@@ -939,27 +977,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
               store_pair(crow, c.n0 + cb + 16 * pp + 8 * half, p.n, row_ok, y[0], y[1]);
           }
         }
-        if constexpr (kLineStores) {
-          // Lanes read what other lanes wrote: keep the compiler from moving
-          // LDS accesses across this point (the hardware runs a wave's LDS
-          // operations in order), here and after the reads below.
-          __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-          __builtin_amdgcn_wave_barrier();
-          // Row rr of the block, 16-byte chunk ch of the wave's 64 columns.
-          const int ch = ol & 7;
-          const int64_t col = c.n0 + wn * 64 + 8 * ch;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int rr = 8 * q + (ol >> 3);
-            const u32x4 v = line_get(rr, ch);
-            const int mr = wm * (BM / 2) + 32 * j + rr;
-            const int64_t gr = c.row_base + mr;
-            if (mr < c.rows_valid && gr >= 0 && gr <= last_row && col < p.n)
-              *reinterpret_cast<u32x4*>(p.c + gr * p.ldc + col) = v;
-          }
-          __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-          __builtin_amdgcn_wave_barrier();
-        }
+        if constexpr (kLineStores) line_flush(c, j, ol, c.n0 + wn * (BN / kWN), p.n);
       }
     }
   };
