@@ -121,12 +121,30 @@ struct IntConst {
   static constexpr int value = V;
 };
 
-// Fused epilogues (element-wise on the fp32 accumulator, before rounding).
-__device__ __forceinline__ float gelu_erf(float x) {  // torch.nn.functional.gelu, exact form
-  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+// Fused epilogues (element-wise on the fp32 accumulator, before rounding to
+// 16 bits).  They run on 128 values per lane per tile while the matrix cores
+// wait, so they use the hardware reciprocal and base-2 exponential (about
+// 1 ulp each) instead of the library's correctly rounded routines.
+__device__ __forceinline__ float exp_neg(float x) {  // e^(-x)
+  return __builtin_amdgcn_exp2f(-1.44269504088896341f * x);
+}
+// erf(z) for z >= 0 by Abramowitz & Stegun, Handbook of Mathematical
+// Functions, formula 7.1.26: 1 - t(a1 + t(a2 + t(a3 + t(a4 + t a5)))) e^(-z^2),
+// t = 1/(1 + p z), |error| <= 1.5e-7.
+__device__ __forceinline__ float erf_pos(float z) {
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * z);
+  const float poly =
+      t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
+  return 1.0f - poly * exp_neg(z * z);
+}
+__device__ __forceinline__ float gelu_erf(float x) {  // torch.nn.functional.gelu, exact (erf) form
+  const float e = erf_pos(fabsf(x) * 0.70710678118654752f);
+  return 0.5f * x * (1.0f + copysignf(e, x));
 }
 __device__ __forceinline__ float silu_mul(float gate, float up) {  // silu(gate) * up
-  return gate / (1.0f + expf(-gate)) * up;
+  // e^(-gate) overflows to inf for gate < -88: the reciprocal is then 0 and
+  // so is the result, as silu's limit is.
+  return gate * __builtin_amdgcn_rcpf(1.0f + exp_neg(gate)) * up;
 }
 
 // Per-expert tile prefix of the derived queue, built in LDS by the whole
