@@ -264,3 +264,68 @@ def test_expert_mlp_baseline_config(cuda_device):
     log(f"cfg4 max abs {err.max().item():.4g} rel rms {rel_rms:.3g}")
     assert err.max().item() <= 2 * tol(case.ffn)
     assert rel_rms <= 1e-2
+
+
+def _activation_probe(values_a, cols_a, n, dtype, device):
+    """One expert whose GEMM output C[r, :] is exactly a chosen pre-activation:
+    A[r, c] = values_a[c][r] for the first columns, B[0] routes column c of A
+    onto the output columns cols_a[c]."""
+    m = values_a[0].numel()
+    k = 64
+    a = torch.zeros(m, k, dtype=dtype)
+    b = torch.zeros(1, k, n, dtype=dtype)
+    for c, (vals, cols) in enumerate(zip(values_a, cols_a)):
+        a[:, c] = vals.to(dtype)
+        b[0, c, cols] = 1.0
+    offs = torch.tensor([0, m], dtype=torch.int32)
+    return a.to(device), b.to(device), offs.to(device)
+
+
+def _wide_inputs(m, lo, hi, seed):
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.linspace(lo, hi, m - 16)
+    x = x + torch.rand(m - 16, generator=gen) * (hi - lo) / m
+    special = torch.tensor([0.0, -0.0, 1e-3, -1e-3, 1e-20, -1e-20, 5.0, -5.0,
+                            hi, lo, 88.0, -88.0, 89.0, -89.0, 0.70710678, -0.70710678])
+    return torch.cat([x, special]).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("block", [256, 128])
+def test_gelu_epilogue_accuracy_over_wide_range(cuda_device, block):
+    """The epilogue's erf (Abramowitz-Stegun 7.1.26 on the hardware exp2 and
+    reciprocal) against float64 torch.gelu: within one bf16 rounding (2^-8
+    relative) plus 2e-6 absolute, over pre-activations in [-100, 100] and the
+    cases where erf saturates."""
+    x = _wide_inputs(512, -100.0, 100.0, seed=1)
+    n = 256
+    a, b, offs = _activation_probe([x], [torch.arange(n)], n, torch.bfloat16, cuda_device)
+    c = mlp._grouped_gemm_ex(a, b, offs, mlp._EPILOGUES["gelu"], n, None, block, False)
+    torch.cuda.synchronize()
+    ref = torch.nn.functional.gelu(x.double())[:, None].expand(-1, n).numpy()
+    got = c.double().cpu().numpy()
+    bound = 2.0 ** -8 * 1.01 * np.abs(ref) + 2e-6
+    bad = np.abs(got - ref) > bound
+    assert not bad.any(), (x[np.nonzero(bad)[0][:5]], got[bad][:5], ref[bad][:5])
+
+
+@pytest.mark.parametrize("block", [256, 128])
+def test_swiglu_epilogue_accuracy_over_wide_range(cuda_device, block):
+    """silu(gate) * up on the hardware exp2 and reciprocal against float64,
+    within one bf16 rounding plus 2e-6 absolute, for gates in [-100, 100]
+    (e^-gate overflows below -88: the result is then 0, silu's limit)."""
+    g = _wide_inputs(512, -100.0, 100.0, seed=2)
+    gen = torch.Generator().manual_seed(3)
+    u = (torch.randn(512, generator=gen) * 3).to(torch.bfloat16)
+    n = 256  # interleaved: columns 64q..64q+31 gate, 64q+32..64q+63 up of outputs 32q..32q+31
+    cols = torch.arange(n)
+    gate_cols = cols[(cols % 64) < 32]
+    up_cols = cols[(cols % 64) >= 32]
+    a, b, offs = _activation_probe([g, u], [gate_cols, up_cols], n, torch.bfloat16, cuda_device)
+    c = mlp._grouped_gemm_ex(a, b, offs, mlp._EPILOGUES["swiglu"], n // 2, None, block, False)
+    torch.cuda.synchronize()
+    gd, ud = g.double(), u.double()
+    ref = (gd * torch.sigmoid(gd) * ud)[:, None].expand(-1, n // 2).numpy()
+    got = c.double().cpu().numpy()
+    bound = 2.0 ** -8 * 1.01 * np.abs(ref) + 2e-6
+    bad = np.abs(got - ref) > bound
+    assert not bad.any(), (g[np.nonzero(bad)[0][:5]], got[bad][:5], ref[bad][:5])
