@@ -56,6 +56,12 @@ extern "C" {
 #define MGG_DTYPE_BF16 0
 #define MGG_DTYPE_FP16 1
 #define MGG_DTYPE_FP8_E4M3 2 /* OCP e4m3 (float8_e4m3fn) operands, BF16 output */
+/* OR'd into the BF16/FP16 dtype of mgg_grouped_gemm and mgg_grouped_gemm_ex:
+ * B is stored [E, N, K] with K contiguous (a linear layer's [out, in] weight,
+ * passed by the reference's callers as its [E, K, N] transposed view), and
+ * ldb_k is the stride between B's N rows (>= K).  Results are bitwise those
+ * of the same values stored [E, K, N].  (Introduced with ABI version 3.) */
+#define MGG_B_KMAJOR 0x100
 
 /* Fused GEMM epilogues (mgg_grouped_gemm_ex). */
 #define MGG_EPI_NONE 0

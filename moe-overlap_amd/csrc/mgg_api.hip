@@ -64,7 +64,7 @@ using mgg::set_error;
 
 extern "C" {
 
-int mgg_abi_version(void) { return 2; }
+int mgg_abi_version(void) { return 3; }
 
 const char* mgg_last_error(void) { return mgg::g_last_error.c_str(); }
 
@@ -179,8 +179,12 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
                       int num_workers, int use_atomic_queue, int32_t* work_counter,
                       hipStream_t st) {
   const bool fp8 = dtype == MGG_DTYPE_FP8_E4M3;
-  if (dtype != MGG_DTYPE_BF16 && dtype != MGG_DTYPE_FP16 && !fp8)
-    return set_error(MGG_ERR_UNSUPPORTED, "dtype must be MGG_DTYPE_BF16 or MGG_DTYPE_FP16");
+  const int base = dtype & ~MGG_B_KMAJOR;
+  const bool kmajor = (dtype & MGG_B_KMAJOR) != 0;  // 16-bit B stored [E, N, K]
+  if (!fp8 && ((base != MGG_DTYPE_BF16 && base != MGG_DTYPE_FP16) || (dtype & ~(MGG_B_KMAJOR | 1)) != 0))
+    return set_error(MGG_ERR_UNSUPPORTED,
+                     "dtype must be MGG_DTYPE_BF16 or MGG_DTYPE_FP16 (optionally | MGG_B_KMAJOR)");
+  const bool b_rows_k = fp8 || kmajor;  // B's rows run along K (N rows of K values)
   if (fp8 && epilogue != MGG_EPI_NONE)
     return set_error(MGG_ERR_UNSUPPORTED, "fp8 takes no fused epilogue");
   if (fp8 && !(block_n == 128 && (block_m == 256 || block_m == 192 || block_m == 128)))
@@ -203,8 +207,9 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   if (epilogue == MGG_EPI_SWIGLU && n_size % 64 != 0)
     return set_error(MGG_ERR_UNSUPPORTED, "SwiGLU needs N (gate and up columns) a multiple of 64");
   const int64_t c_cols = epilogue == MGG_EPI_SWIGLU ? n_size / 2 : n_size;
-  // ldb_k: stride between B's rows (K rows of N values; for fp8, N rows of K values).
-  if (lda < k_size || ldb_k < (fp8 ? k_size : n_size) || ldc < c_cols || ldb_e < 0)
+  // ldb_k: stride between B's rows (K rows of N values; for fp8 and K-major
+  // B, N rows of K values).
+  if (lda < k_size || ldb_k < (b_rows_k ? k_size : n_size) || ldc < c_cols || ldb_e < 0)
     return set_error(MGG_ERR_INVALID, "leading dimensions smaller than the matrix extents");
   if (lda % 8 != 0 || ldb_k % 8 != 0 || ldb_e % 8 != 0 || ldc % 8 != 0)
     return set_error(MGG_ERR_UNSUPPORTED, "strides must be multiples of 8 elements");
@@ -219,7 +224,7 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   // In-tile byte offsets are 32-bit: BM rows of A, K+8 rows of B.
   const int64_t lim = ((int64_t)1 << 31) - 4096;
   const int64_t es = fp8 ? 1 : 2;
-  const int64_t b_span = fp8 ? ((int64_t)block_n * ldb_k + k_size) : (k_size + 8) * ldb_k;
+  const int64_t b_span = b_rows_k ? ((int64_t)block_n * ldb_k + k_size) : (k_size + 8) * ldb_k;
   if ((int64_t)block_m * lda * es + k_size * es >= lim || b_span * es >= lim)
     return set_error(MGG_ERR_UNSUPPORTED, "row strides too large for 32-bit tile offsets");
 

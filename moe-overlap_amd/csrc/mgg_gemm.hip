@@ -27,6 +27,11 @@
 #define MGG_SBK256 32
 #define MGG_NS256 4
 #endif
+// K-major 16-bit B (no A blocks: both operands in a ring of 32-deep stages).
+#ifndef MGG_KM_SBK256
+#define MGG_KM_SBK256 32
+#define MGG_KM_NS256 4
+#endif
 #ifndef MGG_NW256
 #define MGG_NW256 8
 #endif
@@ -90,6 +95,17 @@ struct F16 {
     f16x2 v = {(_Float16)lo, (_Float16)hi};
     return __builtin_bit_cast(uint32_t, v);
   }
+};
+
+// 16-bit operands with B stored [E, N, K]: B's tile rows are loaded like A's
+// (rows of K) and its fragments are plain 16-byte row reads, which hold the
+// same values per lane as the transposing reads of [E, K, N] B, so the MFMA
+// sequence and the results are the same bit for bit.
+struct Bf16K : Bf16 {
+  static constexpr bool kBKMajor = true;
+};
+struct F16K : F16 {
+  static constexpr bool kBKMajor = true;
 };
 
 // OCP fp8 e4m3 operands (v_mfma_f32_32x32x64_f8f6f4, both formats e4m3: lane
@@ -1157,7 +1173,9 @@ int launch_typed(int block_m, int block_n, const GemmParams& p, int workers, hip
   // rows) and as many stages as the LDS budget holds, except the 256x256
   // tile (see MGG_SBK256).  Fused epilogues are compiled for the 256x256 and
   // 128x128 tiles (two 32-column blocks per wave).
-  MGG_CASE(256, 256, MGG_SBK256, MGG_NS256, MGG_NW256)
+  constexpr int kSbk256 = T::kBKMajor ? MGG_KM_SBK256 : MGG_SBK256;
+  constexpr int kNs256 = T::kBKMajor ? MGG_KM_NS256 : MGG_NS256;
+  MGG_CASE(256, 256, kSbk256, kNs256, MGG_NW256)
   MGG_CASE(128, 128, 64, 4, 4)
   if constexpr (EPI == kEpiNone) {
     MGG_CASE(256, 128, 64, 3, 4)
@@ -1219,6 +1237,10 @@ int launch_grouped_gemm(int dtype, int epilogue, int block_m, int block_n, const
     rc = launch_epi<Bf16>(epilogue, block_m, block_n, p, workers, stream);
   else if (dtype == MGG_DTYPE_FP16)
     rc = launch_epi<F16>(epilogue, block_m, block_n, p, workers, stream);
+  else if (dtype == (MGG_DTYPE_BF16 | MGG_B_KMAJOR))
+    rc = launch_epi<Bf16K>(epilogue, block_m, block_n, p, workers, stream);
+  else if (dtype == (MGG_DTYPE_FP16 | MGG_B_KMAJOR))
+    rc = launch_epi<F16K>(epilogue, block_m, block_n, p, workers, stream);
   else if (dtype == MGG_DTYPE_FP8_E4M3 && epilogue == kEpiNone)
     rc = launch_fp8(block_m, block_n, p, workers, stream);
   else

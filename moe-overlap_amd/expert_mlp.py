@@ -201,13 +201,16 @@ def _grouped_gemm_ex(a, b, offsets, epilogue, out_cols, num_sms, block, use_atom
                                        block_n=block, use_atomic_queue=use_atomic_queue)
     M, K = a.shape
     E, _, N = b.shape
-    if a.stride(1) != 1 or b.stride(2) != 1:
-        raise ValueError("operands need unit inner strides")
+    kmajor = b.stride(1) == 1 and b.stride(2) != 1  # [E, K, N] view of [E, N, K] weights
+    if a.stride(1) != 1 or (b.stride(2) != 1 and not kmajor):
+        raise ValueError("operands need unit inner strides (B: along N, or along K)")
+    dtype = _DTYPES[a.dtype] | (nat.MGG_B_KMAJOR if kmajor else 0)
+    ldb_rows = b.stride(2) if kmajor else b.stride(1)
     c = torch.empty(M, out_cols, dtype=a.dtype, device=a.device)
     with torch.cuda.device(a.device):
         nat.check(nat.lib().mgg_grouped_gemm_ex(
-            _DTYPES[a.dtype], epilogue, _p(a), _p(b), _p(c), _p(offsets), M, K, N, E,
-            a.stride(0), b.stride(0), b.stride(1), c.stride(0), block, block,
+            dtype, epilogue, _p(a), _p(b), _p(c), _p(offsets), M, K, N, E,
+            a.stride(0), b.stride(0), ldb_rows, c.stride(0), block, block,
             int(num_sms) if num_sms else 0, 1 if use_atomic_queue else 0, None,
             _stream_ptr(a.device)))
     return c

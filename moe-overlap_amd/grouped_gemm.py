@@ -198,6 +198,18 @@ def _fast_layout(t: torch.Tensor) -> bool:
     return all(t.stride(d) % 8 == 0 for d in range(t.dim() - 1) if t.size(d) > 1)
 
 
+def _kmajor_layout(b: torch.Tensor) -> bool:
+    """b [E, K, N] is a view of [E, N, K] memory (K contiguous: a linear
+    layer's [out, in] weight transposed) that the kernel reads in place: N-row
+    and expert strides multiples of 8 elements, 16-byte aligned base."""
+    _, k, n = b.shape
+    if k < 2 or n < 2 or b.stride(1) != 1 or b.stride(2) < k:
+        return False
+    if b.data_ptr() % 16 != 0 or b.stride(2) % 8 != 0:
+        return False
+    return b.size(0) < 2 or b.stride(0) % 8 == 0
+
+
 def _gemm_operand(t: torch.Tensor) -> torch.Tensor:
     """`t` itself when the kernel can read it in place, else a device copy."""
     if _fast_layout(t):
@@ -231,7 +243,11 @@ def persistent_grouped_gemm(
     [E, K, N], expert_offsets [E+1]; bf16 or fp16; fp32 accumulation; output
     [M, N] in the input dtype (rows outside every expert range are left
     uninitialised; an empty queue zero-fills).  Launches asynchronously on the
-    current stream of a_cat's device.
+    current stream of a_cat's device.  b_expert may be a [E, K, N] view of
+    [E, N, K] memory (K contiguous, e.g. w.transpose(1, 2) of a linear
+    layer's weight, which the reference's Triton kernel reads through its
+    strides): it is read in place, with results bitwise equal to those of the
+    same values stored [E, K, N]; other layouts are copied first.
 
     Extension beyond the reference (which rejects fp8, :357-358): with
     float8_e4m3fn a_cat and b_expert plus a_scale [M] (per token) and b_scale
@@ -290,17 +306,26 @@ def persistent_grouped_gemm(
     k_pad = (k_size + 7) // 8 * 8
     n_pad = (n_size + 7) // 8 * 8
     a_op, b_op = a_cat, b_expert
+    # B stored [E, N, K] is read as it lies (no transposing copy).
+    b_kmajor = k_pad == k_size and n_pad == n_size and _kmajor_layout(b_expert)
     if k_pad != k_size:
         a_op = torch.nn.functional.pad(a_op, (0, k_pad - k_size))
         b_op = torch.nn.functional.pad(b_op, (0, 0, 0, k_pad - k_size))
     if n_pad != n_size:
         b_op = torch.nn.functional.pad(b_op, (0, n_pad - n_size))
     a_op = _gemm_operand(a_op)
-    b_op = _gemm_operand(b_op)
-    # Leading dimensions; a size-1 dimension's stride is never used.
+    if not b_kmajor:
+        b_op = _gemm_operand(b_op)
+    # Leading dimensions; a size-1 dimension's stride is never used.  ldb_k is
+    # the stride between B's rows: K rows, or N rows for K-major B.
     lda = a_op.stride(0) if m_total > 1 else k_pad
-    ldb_k = b_op.stride(1) if k_pad > 1 else n_pad
-    ldb_e = b_op.stride(0) if num_experts > 1 else k_pad * ldb_k
+    if b_kmajor:
+        ldb_k = b_op.stride(2)
+        ldb_e = b_op.stride(0) if num_experts > 1 else n_pad * ldb_k
+    else:
+        ldb_k = b_op.stride(1) if k_pad > 1 else n_pad
+        ldb_e = b_op.stride(0) if num_experts > 1 else k_pad * ldb_k
+    dtype_code = _DTYPE_CODES[a_cat.dtype] | (_nat.MGG_B_KMAJOR if b_kmajor else 0)
     c_op = torch.empty((m_total, n_pad), device=device, dtype=a_cat.dtype)
 
     if queue == "prebuilt":
@@ -313,7 +338,7 @@ def persistent_grouped_gemm(
     off32 = off32.contiguous()
 
     args = (
-        _DTYPE_CODES[a_cat.dtype], _ptr(a_op), _ptr(b_op), _ptr(c_op),
+        dtype_code, _ptr(a_op), _ptr(b_op), _ptr(c_op),
         _ptr(off32), m_total, k_pad, n_pad,
         num_experts, lda, ldb_e, ldb_k, c_op.stride(0),
         _ptr(we), _ptr(wm), _ptr(wn), num_work,

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime this library must share)
 
 LIB_PATH = Path(__file__).resolve().parent / "libmgg.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MGG_OK = 0
 MGG_ERR_INVALID = 1
@@ -23,6 +23,7 @@ MGG_ERR_HIP = 3
 MGG_DTYPE_BF16 = 0
 MGG_DTYPE_FP16 = 1
 MGG_DTYPE_FP8_E4M3 = 2
+MGG_B_KMAJOR = 0x100  # | BF16/FP16: B stored [E, N, K], ldb_k = stride between N rows
 MGG_INT32 = 0
 MGG_INT64 = 1
 # Largest expert count for which the kernels derive the work queue on the

@@ -366,3 +366,63 @@ def test_device_offsets_bit_exact(cuda_device):
                 np.testing.assert_array_equal(got.cpu().numpy(), want)
     wrap = torch.tensor([2**31 - 1, 1, 2**32 + 3], dtype=torch.int64, device=cuda_device)
     assert gg.expert_offsets_from_recv_counts(wrap).tolist() == [0, 2**31 - 1, -(2**31), -(2**31) + 3]
+
+
+KMAJOR_CASES = [
+    # counts, K, N, extra K columns of the [E, N, K] storage (N-row stride K + pad)
+    ([3, 0, 5], 64, 64, 0),
+    ([130, 1, 257], 72, 64, 8),
+    ([0, 0, 513, 0], 256, 136, 0),
+    ([600], 520, 520, 24),
+    ([300, 0, 257, 1, 512], 2056, 264, 0),
+]
+ALL_BLOCKS = [(256, 256), (128, 128), (256, 128), (128, 256), (64, 64), (64, 128), (128, 64),
+              (256, 64), (64, 256)]
+
+
+def kmajor_copy(b, pad):
+    """The values of b [E, K, N] stored [E, N, K + pad] (K contiguous), as an [E, K, N] view."""
+    e, k, n = b.shape
+    store = torch.zeros(e, n, k + pad, dtype=b.dtype, device=b.device)
+    store[:, :, :k] = b.transpose(1, 2)
+    return store[:, :, :k].transpose(1, 2)
+
+
+@pytest.mark.parametrize("case", range(len(KMAJOR_CASES)))
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_kmajor_b_is_read_in_place_bitwise(cuda_device, case, dtype):
+    """B as a [E, K, N] view of [E, N, K] memory (a linear layer's weight
+    transposed, which the reference's Triton kernel reads through its strides)
+    takes the K-major kernels, with no copy, and gives bitwise the result of
+    the same values stored [E, K, N] on every tile and schedule."""
+    counts, k, n, pad = KMAJOR_CASES[case]
+    a, b, offs = make_inputs(counts, k, n, dtype, cuda_device, seed=100 + case, extra_rows=2)
+    b_km = kmajor_copy(b, pad)
+    assert b_km.stride(1) == 1 and b_km.stride(2) == k + pad and gg._kmajor_layout(b_km)
+    mask = torch.from_numpy(covered_rows(offs)).to(cuda_device)
+    for blocks in ALL_BLOCKS:
+        for atomic in (False, True):
+            log(f"kmajor case={case} dtype={dtype} blocks={blocks} atomic={atomic}")
+            c_n = gg.persistent_grouped_gemm(a, b, offs, block_m=blocks[0], block_n=blocks[1],
+                                             use_atomic_queue=atomic)
+            c_k = gg.persistent_grouped_gemm(a, b_km, offs, block_m=blocks[0], block_n=blocks[1],
+                                             use_atomic_queue=atomic)
+            torch.cuda.synchronize()
+            assert torch.equal(c_k[: mask.numel()][mask], c_n[: mask.numel()][mask]), (blocks, atomic)
+        assert_parity(c_k, a, b, offs, k)
+
+
+@pytest.mark.parametrize("epilogue", ["gelu", "swiglu"])
+@pytest.mark.parametrize("block", [256, 128])
+def test_kmajor_b_fused_epilogues_bitwise(cuda_device, epilogue, block):
+    import expert_mlp as mlp
+    counts, k, n = [300, 0, 257, 1, 200], 136, 256
+    a, b, offs = make_inputs(counts, k, n, torch.bfloat16, cuda_device, seed=7, extra_rows=1)
+    b_km = kmajor_copy(b, 16)
+    out = n // 2 if epilogue == "swiglu" else n
+    epi = mlp._EPILOGUES[epilogue]
+    c_n = mlp._grouped_gemm_ex(a, b, offs, epi, out, None, block, True)
+    c_k = mlp._grouped_gemm_ex(a, b_km, offs, epi, out, None, block, True)
+    torch.cuda.synchronize()
+    mask = torch.from_numpy(covered_rows(offs)).to(cuda_device)
+    assert torch.equal(c_k[: mask.numel()][mask], c_n[: mask.numel()][mask])
