@@ -899,7 +899,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
                         const float* y0, const float* y1) {
     const u32x4 v = pack_pair(y0, y1);
     // col already includes 8*half
-    if (row_ok && col < cols) *reinterpret_cast<u32x4*>(crow + col) = v;
+    if (row_ok && col < cols) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(crow + col));
   };
   // Stores through LDS: a wave's output columns of a row are one 64- or
   // 128-byte segment of C, but a store instruction straight from the MFMA
@@ -908,7 +908,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   // conflict-free both ways) and comes back as whole row segments, 8 rows of
   // 128 bytes or 16 of 64 per instruction (32 MiB bursts of such stores
   // measured 30% faster than 32-byte segments; 64-byte ones 19% faster).
-  // The region is free for the whole epilogue:
+  // The LDS region is free for the whole epilogue:
   // * A-block tile: a 4 KiB share of A slot 1.  No DMA is in flight into it
   //   (the last stage's wait retired the zero-fill block the last even stage
   //   sent there) and the next tile first fills it in its first stage, after
@@ -920,6 +920,10 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   // The LDS addresses are derived from an opaque copy of the lane index taken
   // in the epilogue: otherwise the compiler computes them once per kernel and
   // keeps them live through the K loop, which then spills.
+  // C goes out with non-temporal stores: this launch never reads it again, and
+  // left in L2 it would evict A and B lines that other tiles still read
+  // (measured: skewed routing and the atomic schedule 4-5.5% faster, fp8
+  // 3.5-5%).
   constexpr int kOutCols = EPI == kEpiSwiglu ? BN / kWN / 2 : BN / kWN;  // per wave and row
   constexpr int kLineChunks = kOutCols * 2 / 16;  // 16-byte chunks of a wave's row segment
   constexpr bool kLineStores =
@@ -958,7 +962,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
       const int mr = wm * (BM / 2) + 32 * j + rr;
       const int64_t gr = c.row_base + mr;
       if (mr < c.rows_valid && gr >= 0 && gr <= last_row && col < cols)
-        *reinterpret_cast<u32x4*>(p.c + gr * p.ldc + col) = v;
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p.c + gr * p.ldc + col));
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
