@@ -49,9 +49,10 @@ def parse_args():
                    choices=["uniform", "skewed", "cpu_plumbing", "expert_mlp", "fp8"],
                    help="uniform (the metric's config), skewed, cpu_plumbing; expert_mlp and fp8 "
                         "time the BASELINE expert-MLP forward / fp8 GEMM configs instead")
-    # striped by default, as the reference's benchmark (src/bench_triton_grouped_gemm.py:28-32:
-    # --atomic-queue is opt-in); the comparison below times both schedules either way
-    p.add_argument("--mode", default="striped", choices=["atomic", "striped"])
+    # atomic by default, as the reference's API (persistent_grouped_gemm's use_atomic_queue=True,
+    # src/triton_grouped_gemm.py:334; its benchmark script makes it opt-in, :28-32); the
+    # comparison below times both schedules either way
+    p.add_argument("--mode", default="atomic", choices=["atomic", "striped"])
     p.add_argument("--block-m", type=int, default=256)
     p.add_argument("--block-n", type=int, default=256)
     p.add_argument("--num-sms", type=int, default=None)
