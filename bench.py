@@ -2,7 +2,7 @@
 """Benchmark of the persistent expert-grouped GEMM on one MI355X.
 
 A step is one ``persistent_grouped_gemm`` call (the full drop-in API: offsets
-already on the device, output allocation, launch) over the BASELINE metric's
+already on the device, output allocation, launch) over the benchmark metric's
 workload: E=16 experts x 512 routed tokens, K=2048, N=4096, bf16 in, fp32
 accumulate, bf16 out.  Inputs are synthetic (N(0,1) activations, N(0,1/K)
 weights) and resident in HBM before the timed region.
@@ -48,7 +48,7 @@ def parse_args():
     p.add_argument("--workload", default="uniform",
                    choices=["uniform", "skewed", "cpu_plumbing", "expert_mlp", "fp8"],
                    help="uniform (the metric's config), skewed, cpu_plumbing; expert_mlp and fp8 "
-                        "time the BASELINE expert-MLP forward / fp8 GEMM configs instead")
+                        "time the benchmark expert-MLP forward / fp8 GEMM configs instead")
     # atomic by default, as the reference's API (persistent_grouped_gemm's use_atomic_queue=True,
     # src/triton_grouped_gemm.py:334; its benchmark script makes it opt-in, :28-32); the
     # comparison below times both schedules either way
@@ -114,7 +114,7 @@ def median(xs):
 
 
 def expert_mlp_summary(dev, steps: int = 10):
-    """The BASELINE expert-MLP config (8192 tokens top-2 of 16, H 2048, SwiGLU
+    """The benchmark expert-MLP config (8192 tokens top-2 of 16, H 2048, SwiGLU
     F 4096): whole forward (layout, gather, up GEMM + SwiGLU, down GEMM,
     combine) and each launch alone, from HIP events on the current stream."""
     import torch
@@ -162,7 +162,7 @@ def expert_mlp_summary(dev, steps: int = 10):
 
 
 def fp8_summary(dev, steps: int = 20):
-    """The BASELINE fp8 config (E=64, M=24576, K=2048, N=1408, e4m3 with
+    """The benchmark fp8 config (E=64, M=24576, K=2048, N=1408, e4m3 with
     per-token x per-channel scales, bf16 out), HBM-bound by its algorithmic
     bytes: each tile shape and schedule, kernel time from HIP events."""
     import grouped_gemm as gg
@@ -359,7 +359,7 @@ def secondary_main(args, dev):
         "metric": metric, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
-        "data": "synthetic (BASELINE recipe, random init)", "config": config,
+        "data": "synthetic (benchmark recipe, random init)", "config": config,
         "kernel_ms_mean": round(k_mean, 5),
         "roofline": {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
                      "frac": round(achieved / peak, 4),
@@ -373,7 +373,7 @@ def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the grouped GEMM shards by expert; see DESIGN.md).", file=sys.stderr)
+              "(the grouped GEMM shards by expert across GPUs; one GPU's share is what runs here).", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -440,7 +440,7 @@ def main():
 
     extra = {}
     if not args.no_compare:
-        # The other BASELINE configs first, while the card is at its steady clock (the legs below
+        # The other benchmark configs first, while the card is at its steady clock (the legs below
         # load it for seconds; its clock sags under sustained load).
         extra["expert_mlp"] = expert_mlp_summary(dev)
         extra["fp8"] = fp8_summary(dev)

@@ -1,4 +1,4 @@
-"""Synthetic routed-token workloads of the BASELINE configs (fixed seeds).
+"""Synthetic routed-token workloads of the benchmark configurations (fixed seeds).
 
 Counts come from the routing recipes; tensors are N(0,1) activations and
 N(0, 1/K) expert weights.  Tensors are drawn with a torch Generator seeded on
@@ -81,7 +81,7 @@ def topk_routing(tokens: int, experts: int, top_k: int, softmax: bool = True):
 
 @dataclass
 class ExpertMlpCase:
-    """The BASELINE expert-MLP config: T tokens routed top-k over E experts,
+    """The benchmark's expert-MLP configuration: T tokens routed top-k over E experts,
     hidden H, SwiGLU FFN of width F (gate|up 2F interleaved for the fused
     epilogue), weights N(0, 1/fan_in)."""
 
@@ -106,7 +106,7 @@ class ExpertMlpCase:
 def make_expert_mlp_case(tokens: int = 8192, experts: int = 16, top_k: int = 2,
                          hidden: int = 2048, ffn: int = 4096, device=None,
                          dtype: torch.dtype = torch.bfloat16, seed: int = 0) -> ExpertMlpCase:
-    """Synthetic inputs of the expert-MLP config (defaults: BASELINE cfg 4)."""
+    """Synthetic inputs of the expert-MLP configuration (defaults: 8192 tokens, top-2 of 16)."""
     case = ExpertMlpCase(tokens, experts, top_k, hidden, ffn)
     idx, w = topk_routing(tokens, experts, top_k)
     device = torch.device("cpu") if device is None else torch.device(device)
@@ -123,7 +123,7 @@ def make_expert_mlp_case(tokens: int = 8192, experts: int = 16, top_k: int = 2,
 
 @dataclass
 class Fp8Case:
-    """The BASELINE fp8 config: per-token scaled e4m3 activations, per-output-
+    """The benchmark's fp8 configuration: per-token scaled e4m3 activations, per-output-
     channel scaled e4m3 expert weights stored [E, N, K] (K contiguous)."""
 
     counts: torch.Tensor  # int32 [E] (CPU)
@@ -158,7 +158,7 @@ class Fp8Case:
 
 def make_fp8_case(tokens: int = 4096, experts: int = 64, top_k: int = 6, k: int = 2048,
                   n: int = 1408, device=None, seed: int = 0, keep_reference: bool = False) -> Fp8Case:
-    """Synthetic inputs of the fp8 config (defaults: BASELINE cfg 5): counts of
+    """Synthetic inputs of the fp8 configuration (defaults: 4096 tokens, top-6 of 64): counts of
     top-k routing on N(0,1) logits, X ~ N(0,1), W ~ N(0, 1/K), each quantised
     with scale = amax / 448 per token and per output channel."""
     counts = topk_counts(tokens, experts, top_k)
@@ -188,7 +188,7 @@ def make_case(
     seed: int = 0,
     materialize: bool = True,
 ) -> GroupedGemmCase:
-    """One of: cpu_plumbing (cfg 1), uniform (cfg 2), skewed (cfg 3)."""
+    """One of: cpu_plumbing (fp32, E=8), uniform (E=16, 512 rows each), skewed (16384 rows)."""
     if name == "cpu_plumbing":
         case = GroupedGemmCase(name, torch.full((8,), 128, dtype=torch.int32), 512, 1024)
     elif name == "uniform":

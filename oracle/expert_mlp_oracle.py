@@ -11,7 +11,7 @@ Functions and what pins each one (tests/test_oracle_mlp.py):
   cumsum offsets, inv_perm), over all top-k slots at once.  Pinned by a
   counting-sort loop written independently, by the permutation invariants
   (positions are a bijection onto [0, M), expert-major, stable in assignment
-  order within an expert) and by the per-expert counts of the BASELINE
+  order within an expert) and by the per-expert counts of the benchmark
   expert-MLP and fp8 routings in tests/golden/routing_counts.json.
 * ``gather_rows`` / ``combine_rows`` -- train:224 (grouped_tokens =
   valid_tokens[perm]) and train:245-246 with :340-341 (out[valid] =
@@ -19,7 +19,7 @@ Functions and what pins each one (tests/test_oracle_mlp.py):
   per-token loops.
 * ``expert_mlp`` -- the expert computation of train:239-243 (GELU on a
   single W1, the reference's ExpertMLP :86-93) and the SwiGLU variant of the
-  BASELINE expert-MLP config, in float64 via the permuted grouped form.
+  benchmark's expert-MLP configuration, in float64 via the permuted grouped form.
   Pinned against a per-token loop, and (GELU) against torch's own
   ``F.gelu(x @ w1) @ w2`` per expert on the CPU.
 * ``interleave_gate_up`` -- the gate|up column layout mgg_grouped_gemm_ex

@@ -13,7 +13,7 @@ Functions and what pins each one (tests/test_oracle_*.py):
 * ``build_work_queue`` -- reference :240-297 (vectorised like the reference:
   repeat + local position).  Pinned by a brute-force triple loop on random
   inputs, by the coverage invariant (every expert row x column is covered by
-  exactly one tile), by the queue lengths quoted for the BASELINE configs, and
+  exactly one tile), by the queue lengths of the benchmark configurations, and
   by hand-enumerated cases.
 * ``grouped_gemm`` -- reference :446-457 (per-expert loop), computed in fp32 or
   fp64.  Pinned by a brute-force scalar triple loop on tiny inputs, one-hot

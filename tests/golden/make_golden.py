@@ -1,6 +1,6 @@
 """Writes the committed fixtures in tests/golden/ (run from the repo root).
 
-* ``routing_counts.json`` -- per-expert counts of the BASELINE configs, from
+* ``routing_counts.json`` -- per-expert counts of the benchmark configs, from
   their routing recipes (the skewed recipe reproduces the counts pinned in the
   build's survey).
 * ``queues.npz`` -- expert offsets and the (expert, tile_m, tile_n) queue of

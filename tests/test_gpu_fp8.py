@@ -8,7 +8,7 @@ exact fp8 values, accumulates in fp32 and rounds once to bf16, so against the
 decoded reference |C - ref| <= 2^-8 |ref| + 2^-16 * mag, where mag =
 a_scale * b_scale * sum_k |a_k| |b_k| bounds the accumulation's rounding
 (outputs near zero come from partial sums ~1e4 times larger).  Against the
-unquantised fp32 GEMM the BASELINE north_star bound applies: relative
+unquantised fp32 GEMM the benchmark's stated bound applies: relative
 (Frobenius) error <= 5e-2.
 """
 import math
@@ -118,7 +118,7 @@ def test_fp8_work_counter_and_errors(cuda_device):
 
 
 def test_fp8_baseline_config(cuda_device):
-    """BASELINE fp8 config: E=64, M=24576 (top-6 of 4096 tokens), K=2048,
+    """benchmark fp8 config: E=64, M=24576 (top-6 of 4096 tokens), K=2048,
     N=1408; against the decoded-fp8 fp32 product per expert on the GPU and
     against the unquantised fp32 GEMM (north_star: relative error <= 5e-2).
     The default tile here is 192x128; 256x128 and 128x128 must give the same

@@ -1,13 +1,13 @@
 """GPU parity of the HIP grouped GEMM (through libmgg's C ABI) against the CPU
 oracle, plus the kernel's scheduling and counter semantics.
 
-Tolerance: max |C - C_fp32| <= 2e-2 * sqrt(K / 512) for
+Tolerance (benchmark's stated): max |C - C_fp32| <= 2e-2 * sqrt(K / 512) for
 bf16/fp16 outputs against an fp32/fp64 reference on the same (already
 rounded) inputs, over every row inside an expert range.  K is floored at 512
 in the formula: with N(0, 1/K) weights the outputs are O(1) at every K, and
 rounding them to bf16 alone costs up to half an ulp, 2^-6 = 0.0156 for
 |y| in [4, 8), which is above 2e-2 * sqrt(K/512) for K < 512.  Every
-BASELINE config has K >= 512, where the formula applies unchanged.
+benchmark config has K >= 512, where the formula applies unchanged.
 """
 import ctypes
 import math

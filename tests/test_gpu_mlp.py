@@ -240,7 +240,7 @@ def test_expert_mlp_random_shapes(cuda_device, seed):
 
 
 def test_expert_mlp_baseline_config(cuda_device):
-    """BASELINE expert-MLP config (8192 tokens, top-2 of 16, H 2048, SwiGLU F
+    """benchmark expert-MLP config (8192 tokens, top-2 of 16, H 2048, SwiGLU F
     4096) against an fp32 torch computation of the same routed MLP."""
     log("mlp cfg4")
     case = workloads.make_expert_mlp_case(device=cuda_device)

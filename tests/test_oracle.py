@@ -100,7 +100,7 @@ def test_queue_covers_each_expert_element_exactly_once(counts, n_size, bm, bn):
 
 
 def test_queue_lengths_of_baseline_configs():
-    # Queue lengths quoted for the BASELINE configs (computed independently there).
+    # Queue lengths quoted for the benchmark configs (computed independently there).
     counts = json.loads((GOLDEN / "routing_counts.json").read_text())
     offs = {k: orc.expert_offsets_from_recv_counts(v) for k, v in counts.items()}
     assert orc.queue_length(offs["cpu_plumbing"], 1024, 128, 128) == 64
