@@ -112,6 +112,12 @@ def gemm_call(**over):
     (dict(e=4096), nat.MGG_ERR_UNSUPPORTED, b"2048 experts"),
     (dict(nw=5), nat.MGG_ERR_INVALID, b"null work queue"),
     (dict(workers=70000), nat.MGG_ERR_INVALID, b"num_workers"),
+    # K-major B: the flag is for 16-bit dtypes only, and ldb_k is then the stride between N
+    # rows, so it must cover K (64 covers N = 64 but not K = 128).
+    (dict(dtype=nat.MGG_DTYPE_FP8_E4M3 | nat.MGG_B_KMAJOR), nat.MGG_ERR_UNSUPPORTED, b"dtype"),
+    (dict(dtype=nat.MGG_DTYPE_BF16 | 0x200), nat.MGG_ERR_UNSUPPORTED, b"dtype"),
+    (dict(dtype=nat.MGG_DTYPE_BF16 | nat.MGG_B_KMAJOR, k=128, lda=128, ldb_k=64, ldb_e=64 * 128),
+     nat.MGG_ERR_INVALID, b"leading"),
 ])
 def test_gemm_validation_rejects_before_launch(over, code, text):
     assert gemm_call(**over) == code
