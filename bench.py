@@ -177,9 +177,9 @@ def fp8_summary(dev, steps: int = 20):
     out = {"config": f"E={case.num_experts}, M={case.m}, K={case.k}, N={case.n}, e4m3 in, bf16 out",
            "algorithmic_bytes": t_bytes, "t_bound_us": round(max(t_flop_bound, t_hbm_bound) * 1e6, 2),
            "runs": {}}
-    out["default_tile"] = f"{gg._default_fp8_block_m(case.m, case.num_experts)}x128"
+    out["default_tile"] = "{}x{}".format(*gg._default_fp8_blocks(case.m, case.num_experts))
     best = None
-    for bm, bn in ((256, 128), (192, 128), (128, 128)):
+    for bm, bn in ((256, 256), (256, 128), (192, 128), (128, 128)):
         for mode in ("striped", "atomic"):
             fn = lambda: gg.persistent_grouped_gemm(case.a, b_kn, offs, block_m=bm, block_n=bn,
                                                     use_atomic_queue=mode == "atomic",
@@ -316,8 +316,8 @@ def secondary_main(args, dev):
         case = workloads.make_fp8_case(device=dev)
         offs = gg.expert_offsets_from_recv_counts(case.counts, device=dev)
         b_kn = case.b_nk.transpose(1, 2)
-        # The library's default fp8 tile (192x128 here) unless a tile is named.
-        bm, bn = ((gg._default_fp8_block_m(case.m, case.num_experts), 128)
+        # The library's default fp8 tile (256x256 here) unless another tile is named.
+        bm, bn = ((gg._default_fp8_blocks(case.m, case.num_experts))
                   if (args.block_m, args.block_n) == (256, 256) else (args.block_m, args.block_n))
         step = lambda: gg.persistent_grouped_gemm(case.a, b_kn, offs, num_sms=args.num_sms,
                                                   block_m=bm, block_n=bn,
@@ -328,7 +328,8 @@ def secondary_main(args, dev):
         config = {"workload": f"fp8: E={case.num_experts}, M={case.m}, K={case.k}, N={case.n}",
                   "mode": args.mode, "block_m": bm, "block_n": bn}
         config_blocks = (bm, bn)
-        kernel = f"grouped_gemm_kernel<{bm},{bn},128,{4 if bm == 128 else 3},8,Fp8,0>"
+        stages = 2 if (bm, bn) == (256, 256) else (4 if bm == 128 else 3)
+        kernel = f"grouped_gemm_kernel<{bm},{bn},128,{stages},8,Fp8,0>"
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()

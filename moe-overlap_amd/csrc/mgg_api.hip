@@ -187,8 +187,9 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   const bool b_rows_k = fp8 || kmajor;  // B's rows run along K (N rows of K values)
   if (fp8 && epilogue != MGG_EPI_NONE)
     return set_error(MGG_ERR_UNSUPPORTED, "fp8 takes no fused epilogue");
-  if (fp8 && !(block_n == 128 && (block_m == 256 || block_m == 192 || block_m == 128)))
-    return set_error(MGG_ERR_UNSUPPORTED, "fp8 tiles are 256x128, 192x128 and 128x128");
+  if (fp8 && !((block_n == 128 && (block_m == 256 || block_m == 192 || block_m == 128)) ||
+              (block_m == 256 && block_n == 256)))
+    return set_error(MGG_ERR_UNSUPPORTED, "fp8 tiles are 256x256, 256x128, 192x128 and 128x128");
   if (epilogue != MGG_EPI_NONE && epilogue != MGG_EPI_GELU && epilogue != MGG_EPI_SWIGLU)
     return set_error(MGG_ERR_INVALID, "epilogue must be MGG_EPI_NONE, MGG_EPI_GELU or MGG_EPI_SWIGLU");
   const bool block_ok = (block_m == 64 || block_m == 128 || block_m == 256) &&

@@ -602,8 +602,13 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   f32x16 acc[kNB][kMB];
   // Fragments are double-buffered by the parity of the K step's global index
   // (k0/16): buffer f holds the step being multiplied while the other fills.
+  // kASingle (the fp8 256x256 tile, whose double-buffered 32-byte fragments
+  // do not fit beside its accumulators): one A buffer; the MFMAs go by A
+  // block, and each block's fragment of the next K step is read as soon as
+  // that block's MFMAs have issued, a K step before it is needed.
+  constexpr bool kASingle = T::kScaled && BM == 256 && BN == 256 && !kABlk && kMB == 4;
   using Frag = typename T::Frag;
-  Frag fa[2][kMB];
+  Frag fa[kASingle ? 1 : 2][kMB];
   Frag fb[2][kNB];
   // One fragment from kFragChunks 16-byte LDS reads at byte offsets off[q] + delta.
   auto read_rows = [&](const uint32_t* off, uint32_t delta) {
@@ -617,7 +622,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     return v;
   };
   auto read_a = [&](int f, int buf, int kk, int j) {
-    fa[f][j] = read_rows(a_off[0][kk], buf * kASlot + 32 * kALdsRow * j);
+    fa[kASingle ? 0 : f][j] = read_rows(a_off[0][kk], buf * kASlot + 32 * kALdsRow * j);
   };
   auto read_b = [&](int f, int buf, int kk, int i) {
     if constexpr (T::kBKMajor) {
@@ -639,10 +644,14 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     fb[f][i] = v;
   };
   // Half `part` of the fragments of K step kk of LDS buffer `buf`, into fragment buffer f.
-  auto read_kstep = [&](int f, int buf, int kk, int part) {
+  // with_a = 0: B only (kASingle reads A by block beside the MFMAs); 1: both;
+  // -1: both unless kASingle.
+  auto read_kstep = [&](int f, int buf, int kk, int part, int with_a = -1) {
+    if (with_a == 1 || (with_a < 0 && !kASingle)) {
 #pragma unroll
-    for (int j = part * kMB / 2; j < (part + 1) * kMB / 2 + (kMB == 1 && part == 0); ++j)
-      read_a(f, buf, kk, j);
+      for (int j = part * kMB / 2; j < (part + 1) * kMB / 2 + (kMB == 1 && part == 0); ++j)
+        read_a(f, buf, kk, j);
+    }
 #pragma unroll
     for (int i = part * kNB / 2; i < (part + 1) * kNB / 2 + (kNB == 1 && part == 0); ++i)
       read_b(f, buf, kk, i);
@@ -651,8 +660,9 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     constexpr int kPer = kMB * kNB;
 #pragma unroll
     for (int q = g * kPer / 4; q < (g + 1) * kPer / 4; ++q) {
-      const int i = q / kMB, j = q % kMB;
-      acc[i][j] = T::mfma(fb[f][i], fa[f][j], acc[i][j]);
+      // kASingle: group g is A block g against every B block.
+      const int i = kASingle ? q % kNB : q / kMB, j = kASingle ? q / kNB : q % kMB;
+      acc[i][j] = T::mfma(fb[f][i], fa[kASingle ? 0 : f][j], acc[i][j]);
     }
   };
 
@@ -686,6 +696,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         mfma_group((p0 + kk) & 1, g);
+        if constexpr (kASingle) read_a(0, buf, kk + 1, g);
         if (g < 2) read_kstep((p0 + kk + 1) & 1, buf, kk + 1, g);
         if (issue) dma_share(kk * 4 + g, next_stage);
         __builtin_amdgcn_sched_barrier(0);
@@ -711,13 +722,17 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     wait_stage(kt + 1, issued);
     __syncthreads();
     const int nbuf = (kt + 1) % kStages;
+    if constexpr (kASingle) read_a(0, nbuf, 0, 0);
     mfma_group(f_last, 1);
+    if constexpr (kASingle) read_a(0, nbuf, 0, 1);
     read_kstep(f_next, nbuf, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     mfma_group(f_last, 2);
+    if constexpr (kASingle) read_a(0, nbuf, 0, 2);
     read_kstep(f_next, nbuf, 0, 1);
     __builtin_amdgcn_sched_barrier(0);
     mfma_group(f_last, 3);
+    if constexpr (kASingle) read_a(0, nbuf, 0, 3);
     __builtin_amdgcn_sched_barrier(0);
   };
   auto last_stage = [&](auto P0, int kt) {
@@ -853,8 +868,8 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
       return;
     }
     if (nk > 0) {
-      read_kstep(0, 0, 0, 0);
-      read_kstep(0, 0, 0, 1);
+      read_kstep(0, 0, 0, 0, 1);
+      read_kstep(0, 0, 0, 1, 1);
     }
     int kt = 0;
     if constexpr (kSteps % 2 == 0) {  // every stage starts on fragment buffer 0
@@ -1212,11 +1227,12 @@ int launch_fp8(int block_m, int block_n, const GemmParams& p, int workers, hipSt
                        dim3(workers), dim3(NW_ * 64), 0, stream, p);                          \
     return MGG_OK;                                                                            \
   }
+  MGG_CASE(256, 256, 128, 2, MGG_FP8_NW)
   MGG_CASE(256, 128, 128, 3, MGG_FP8_NW)
   MGG_CASE(192, 128, 128, 3, MGG_FP8_NW)
   MGG_CASE(128, 128, 128, 4, MGG_FP8_NW)
 #undef MGG_CASE
-  return set_error(MGG_ERR_UNSUPPORTED, "fp8 tiles are 256x128, 192x128 and 128x128");
+  return set_error(MGG_ERR_UNSUPPORTED, "fp8 tiles are 256x256, 256x128, 192x128 and 128x128");
 }
 
 template <class T>

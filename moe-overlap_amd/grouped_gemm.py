@@ -360,19 +360,24 @@ def persistent_grouped_gemm(
 _FP8_BLOCK_M = (256, 192, 128)
 
 
-def _default_fp8_block_m(m_total: int, num_experts: int) -> int:
-    """fp8 tile height by the average rows per expert (top-k routing spreads
-    the counts around it): 128 up to 128 rows, 256 for 129-256 (one tile holds
-    most experts), 192 for 257-384 (two tiles, where 256 would pad to 512),
-    256 above.  Measured on MI355X at E=64, K=2048, N=1408, striped order:
-    averages 96 / 192 / 281 / 384 / 516 / 768 run fastest at 128 / 256 / 192 /
-    192 / 256 (tie with 192) / 256."""
+def _default_fp8_blocks(m_total: int, num_experts: int) -> Tuple[int, int]:
+    """fp8 tile by the average rows per expert (top-k routing spreads the
+    counts around it): 128x128 up to 128 rows, 256x128 for 129-256 (one tile
+    holds most experts), 256x256 above.  Measured on MI355X at E=64, K=2048,
+    N=1408, HIP-event medians (striped / atomic, µs): 96 rows 128x128
+    43.2 / 45.6 against 256x256 58.6 / 57.4; 192 rows 256x128 55.4 / 60.4,
+    256x256 59.5 / 59.0; 281 rows 256x256 81.9 / 86.9 against 192x128
+    84.6 / 91.7; 384 rows 85.9 / 94.5 against 103.1 / 112.9; 515 rows
+    111.5 / 122.8 against 256x128 130.3 / 136.5; 768 rows 190.7 / 190.2
+    against 185.7 / 202.8.  The 256x256 tile moves 40% fewer bytes per FLOP
+    than 192x128, and the K loop is bound by the L2 requests a CU keeps in
+    flight."""
     avg = -(-m_total // max(num_experts, 1))
     if avg <= 128:
-        return 128
-    if 256 < avg <= 384:
-        return 192
-    return 256
+        return 128, 128
+    if avg <= 256:
+        return 256, 128
+    return 256, 256
 
 
 def _persistent_grouped_gemm_fp8(a_cat, b_expert, expert_offsets, a_scale, b_scale, num_sms,
@@ -390,10 +395,11 @@ def _persistent_grouped_gemm_fp8(a_cat, b_expert, expert_offsets, a_scale, b_sca
     device = a_cat.device
     dev_index = device.index if device.index is not None else torch.cuda.current_device()
     if block_m is None or block_n is None:
-        block_m = block_m or _default_fp8_block_m(m_total, num_experts)
-        block_n = block_n or 128
-    if block_n != 128 or block_m not in _FP8_BLOCK_M:
-        raise ValueError("fp8 tiles are block_m x block_n = 256x128, 192x128 or 128x128.")
+        dm, dn = _default_fp8_blocks(m_total, num_experts)
+        block_m = block_m or dm
+        block_n = block_n or dn
+    if not ((block_n == 128 and block_m in _FP8_BLOCK_M) or (block_m, block_n) == (256, 256)):
+        raise ValueError("fp8 tiles are block_m x block_n = 256x256, 256x128, 192x128 or 128x128.")
     if num_sms is None:
         num_sms = _cu_count(dev_index)
     counter_dev = None

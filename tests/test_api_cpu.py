@@ -74,11 +74,11 @@ def test_flops_helper():
     assert gg.grouped_gemm_flops([0, 5, 3], 8, 8) == 2 * 5 * 64  # negative counts add nothing
 
 
-@pytest.mark.parametrize("avg,want", [(1, 128), (100, 128), (128, 128), (129, 256), (192, 256),
-                                      (256, 256), (257, 192), (384, 192), (385, 256),
-                                      (512, 256), (4096, 256)])
-def test_default_fp8_tile_height(avg, want):
-    """128 up to 128 rows per expert, 192 for 257-384, else 256; the fp8
-    baseline config (64 experts, 24576 rows: 384 per expert) takes 192."""
-    assert gg._default_fp8_block_m(avg * 64, 64) == want
-    assert gg._default_fp8_block_m(0, 0) == 128
+@pytest.mark.parametrize("avg,want", [(1, (128, 128)), (100, (128, 128)), (128, (128, 128)),
+                                      (129, (256, 128)), (192, (256, 128)), (256, (256, 128)),
+                                      (257, (256, 256)), (384, (256, 256)), (4096, (256, 256))])
+def test_default_fp8_tile(avg, want):
+    """128x128 up to 128 rows per expert, 256x128 for 129-256, else 256x256;
+    the fp8 benchmark config (64 experts, 24576 rows: 384 per expert) takes 256x256."""
+    assert gg._default_fp8_blocks(avg * 64, 64) == want
+    assert gg._default_fp8_blocks(0, 0) == (128, 128)

@@ -56,7 +56,7 @@ def assert_close_fp8(c, a, sa, b, sb, offs):
     assert np.all(err <= bound), float((err - bound).max())
 
 
-@pytest.mark.parametrize("block_m,block_n", [(256, 128), (192, 128), (128, 128)])
+@pytest.mark.parametrize("block_m,block_n", [(256, 256), (256, 128), (192, 128), (128, 128)])
 @pytest.mark.parametrize("atomic", [False, True])
 def test_fp8_small_ragged(cuda_device, block_m, block_n, atomic):
     log(f"fp8 small {block_m}x{block_n} atomic={atomic}")
@@ -80,10 +80,10 @@ def test_fp8_random_shapes(cuda_device, seed):
     counts[rng.random(e) < 0.15] = 1
     k = int(rng.integers(1, 90)) * (16 if seed % 2 == 0 else 7)
     n = int(rng.integers(1, 60)) * (8 if seed % 2 == 0 else 5)
-    bm = (256, 192, 128)[seed % 3]
-    log(f"fp8 random seed={seed} counts={counts.tolist()} K={k} N={n} block_m={bm}")
+    bm, bn = ((256, 128), (192, 128), (128, 128), (256, 256))[seed % 4]
+    log(f"fp8 random seed={seed} counts={counts.tolist()} K={k} N={n} block={bm}x{bn}")
     a, sa, b, sb, offs = fp8_inputs(counts.tolist(), k, n, seed=seed, device=cuda_device)
-    outs = [gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, block_m=bm, block_n=128,
+    outs = [gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, block_m=bm, block_n=bn,
                                        use_atomic_queue=atomic, a_scale=sa, b_scale=sb,
                                        num_sms=int(rng.integers(1, 300)))
             for atomic in (False, True)]
@@ -112,7 +112,7 @@ def test_fp8_work_counter_and_errors(cuda_device):
     assert int(wc.item()) == 2 * 3 * 2 + 7  # W = sum ceil(300/128) * ceil(256/128)
     with pytest.raises(ValueError, match="a_scale"):
         gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs)
-    with pytest.raises(ValueError, match="256x128, 192x128 or 128x128"):
+    with pytest.raises(ValueError, match="256x256, 256x128, 192x128 or 128x128"):
         gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, block_m=64, block_n=64,
                                    a_scale=sa, b_scale=sb)
 
@@ -121,18 +121,18 @@ def test_fp8_baseline_config(cuda_device):
     """benchmark fp8 config: E=64, M=24576 (top-6 of 4096 tokens), K=2048,
     N=1408; against the decoded-fp8 fp32 product per expert on the GPU and
     against the unquantised fp32 GEMM (north_star: relative error <= 5e-2).
-    The default tile here is 192x128; 256x128 and 128x128 must give the same
+    The default tile here is 256x256; 256x128, 128x128 and 192x128 must give the same
     bits (each output's K sum runs in the same order whatever the tile height)."""
     log("fp8 cfg5")
     case = workloads.make_fp8_case(device=cuda_device, keep_reference=True)
     offs = gg.expert_offsets_from_recv_counts(case.counts, device=cuda_device)
-    assert gg._default_fp8_block_m(case.m, case.num_experts) == 192
+    assert gg._default_fp8_blocks(case.m, case.num_experts) == (256, 256)
     c = gg.persistent_grouped_gemm(case.a, case.b_nk.transpose(1, 2), offs,
                                    a_scale=case.a_scale, b_scale=case.b_scale)
-    for bm in (256, 128):
+    for bm, bn in ((256, 128), (128, 128), (192, 128)):
         other = gg.persistent_grouped_gemm(case.a, case.b_nk.transpose(1, 2), offs, block_m=bm,
-                                           block_n=128, a_scale=case.a_scale, b_scale=case.b_scale)
-        assert torch.equal(c, other), bm
+                                           block_n=bn, a_scale=case.a_scale, b_scale=case.b_scale)
+        assert torch.equal(c, other), (bm, bn)
     c = c.float()
     o = offs.cpu().tolist()
     num = den = unq_num = 0.0
