@@ -96,7 +96,7 @@ def recorded_traffic(mode, workload, block_m, block_n):
     (calibrated against a plain copy), when one covers this configuration; else None."""
     if workload == "uniform" and (block_m, block_n) == (256, 256):
         path, key = PROFILE_SUMMARY, f"traffic_bytes_per_launch_{mode}:"
-    elif workload == "fp8" and (block_m, block_n) in ((256, 128), (192, 128)):
+    elif workload == "fp8" and (block_m, block_n) in ((256, 256), (256, 128), (192, 128)):
         path, key = FP8_PROFILE_SUMMARY, f"traffic_bytes_per_launch_fp8_{block_m}x{block_n}_{mode}:"
     else:
         return None
