@@ -183,8 +183,9 @@ int mgg_grouped_gemm_ex(int dtype, int epilogue, const void* a, const void* b, v
  *   a_scale [M], b_scale [E, N] (row stride N): fp32 on the device
  *   c  [M, N]     BF16, row stride ldc
  * Queue, schedules, work_counter and empty-queue behaviour as in
- * mgg_grouped_gemm (queue derived on the device).  Tiles 256x128, 192x128
- * and 128x128; K, lda, ldb_n, ldb_e multiples of 16; N, ldc multiples of 8.
+ * mgg_grouped_gemm (queue derived on the device).  Tiles 256x256, 256x128,
+ * 192x128 and 128x128; K, lda, ldb_n, ldb_e multiples of 16; N, ldc
+ * multiples of 8.
  * (Introduced with ABI version 2.)
  */
 int mgg_grouped_gemm_fp8(const void* a, const void* b, void* c, const int32_t* expert_offsets,

@@ -1215,11 +1215,11 @@ int launch_typed(int block_m, int block_n, const GemmParams& p, int workers, hip
 }
 
 // fp8: 128-byte rows of K (K-wide 128 stages, two 64-deep MFMA steps), eight
-// waves (two per SIMD) on 256x128, 192x128 and 128x128 tiles.  192 rows fit
-// experts of 300-400 rows (two tiles, little padding) and give a launch more,
-// smaller tiles to balance over the CUs.  A 256x256 tile does not
-// fit: its 32-byte fp8 fragments, double-buffered, and its accumulators need
-// more than the 256 registers a wave has at two waves per SIMD.
+// waves (two per SIMD) on 256x256, 256x128, 192x128 and 128x128 tiles.  The
+// 256x256 tile makes the fewest L2 requests per FLOP; it fits the 256
+// registers a wave has at two waves per SIMD only with its A fragments
+// single-buffered (kASingle).  The narrower tiles suit experts of up to 256
+// rows, where a 256x256 tile would be mostly padding.
 int launch_fp8(int block_m, int block_n, const GemmParams& p, int workers, hipStream_t stream) {
 #define MGG_CASE(BM_, BN_, SBK_, NS_, NW_)                                                    \
   if (block_m == BM_ && block_n == BN_) {                                                    \
