@@ -7,14 +7,23 @@ workload: E=16 experts x 512 routed tokens, K=2048, N=4096, bf16 in, fp32
 accumulate, bf16 out.  Inputs are synthetic (N(0,1) activations, N(0,1/K)
 weights) and resident in HBM before the timed region.
 
-Prints ONE JSON line.  ``value`` is TFLOP/s over the timed steps (wall clock
-between two device synchronisations, algorithmic FLOPs 2*M*K*N);
-``roofline.achieved`` is the same FLOPs over the kernel's mean launch time from
-HIP events on the launch stream, recorded in a second pass of the same steps
-(event records are stream commands of their own and stay out of the wall
-clock).  Extra fields compare striped and atomic scheduling under uniform and
-skewed routing, a cache-cold launch time, the per-expert torch loop on the GPU,
-and the CPU oracle on the host's cores.
+Protocol:
+1. ``--warmup`` untimed steps, then the clock is settled whatever ``--warmup``
+   says: the card idles at a low clock and takes tens of milliseconds of work
+   to reach its sustained clock, so steps run in windows of 10 (HIP events
+   around each) until at least 50 ms of GPU time has passed and two
+   consecutive windows' medians agree within 2% (``settle_*`` fields).
+2. Exactly ``--steps`` steps between two device synchronisations: ``value`` is
+   the algorithmic FLOPs (2*M*K*N) of those steps over that wall time.
+3. A pass of max(steps, 50) launches with HIP events around each (event
+   records are stream commands of their own, so they stay out of step 2):
+   ``kernel_ms_median`` / ``_min`` / ``_mean``; ``roofline.achieved`` is the
+   FLOPs over the median launch time.  The shader clock is sampled beside it.
+
+Extra fields compare striped and atomic scheduling under uniform and skewed
+routing, the reference's explicit 128x128 request, a cache-cold launch, the
+per-expert torch loop on the GPU, the expert-MLP and fp8 configs, and the
+per-expert torch loop on the host's cores (``cpu_baseline``).
 """
 from __future__ import annotations
 
@@ -22,8 +31,8 @@ import argparse
 import json
 import math
 import os
-import platform
 import sys
+import threading
 import time
 from pathlib import Path
 
@@ -41,10 +50,8 @@ KERNEL_NAME = "grouped_gemm_kernel<256,256,32,4,8,Bf16,0>"
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    # The card idles at a low clock and takes tens of milliseconds of work to reach its steady
-    # clock, so the default warmup (~30 ms of launches) ends in steady state.
     p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--workload", default="uniform",
                    choices=["uniform", "skewed", "cpu_plumbing", "expert_mlp", "fp8"],
                    help="uniform (the metric's config), skewed, cpu_plumbing; expert_mlp and fp8 "
@@ -53,18 +60,32 @@ def parse_args():
     # src/triton_grouped_gemm.py:334; its benchmark script makes it opt-in, :28-32); the
     # comparison below times both schedules either way
     p.add_argument("--mode", default="atomic", choices=["atomic", "striped"])
-    p.add_argument("--block-m", type=int, default=256)
-    p.add_argument("--block-n", type=int, default=256)
+    # The requested tile (the reference's block_m/block_n, default 128x128): it sets the queue
+    # whose length the work counter reports; the kernel computes with --kernel-tile.
+    p.add_argument("--block-m", type=int, default=128)
+    p.add_argument("--block-n", type=int, default=128)
+    p.add_argument("--kernel-tile", default=None,
+                   help="compiled tile BMxBN to compute with (default: the library's choice)")
     p.add_argument("--num-sms", type=int, default=None)
     p.add_argument("--no-compare", action="store_true", help="skip the schedule/routing comparison")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU oracle sample budget")
+    p.add_argument("--cpu-seconds", type=float, default=12.0,
+                   help="CPU baseline budget (cfg 1 and the fp32-upcast metric config together)")
     p.add_argument("--profile-only", action="store_true",
-                   help="only the warmup and timed steps (for rocprofv3 runs)")
+                   help="only the warmup, settle and timed steps (for rocprofv3 runs)")
+    p.add_argument("--no-settle", action="store_true", help="skip the clock-settling phase")
     p.add_argument("--calibrate-copy-mib", type=int, default=0,
                    help="instead of the GEMM, run --steps plain device copies of this many MiB "
                         "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return p.parse_args()
+
+
+def median(xs):
+    ys = sorted(xs)
+    if not ys:
+        return float("nan")
+    h = len(ys) // 2
+    return ys[h] if len(ys) % 2 else 0.5 * (ys[h - 1] + ys[h])
 
 
 def event_times_ms(fn, iters, flush=None):
@@ -85,19 +106,100 @@ def event_times_ms(fn, iters, flush=None):
     return [s.elapsed_time(e) for s, e in times]
 
 
+def settle_clock(fn, min_ms=50.0, window=10, rel=0.02, max_s=5.0):
+    """Runs fn in windows of `window` launches until at least `min_ms` of GPU
+    time has passed and two consecutive windows' median launch times agree
+    within `rel` (the clock has stopped ramping), or `max_s` of wall time."""
+    t0 = time.perf_counter()
+    total_ms, launches, prev, last = 0.0, 0, None, None
+    while True:
+        ts = event_times_ms(fn, window)
+        total_ms += sum(ts)
+        launches += window
+        last = median(ts)
+        done = total_ms >= min_ms and prev is not None and abs(last - prev) <= rel * last
+        if done or time.perf_counter() - t0 > max_s:
+            return {"settle_launches": launches, "settle_ms": round(total_ms, 2),
+                    "settle_window_ms_median": round(last, 5), "settled": bool(done)}
+        prev = last
+
+
+class ClockSampler:
+    """Samples the GPU's current shader (GFX) clock through amdsmi in a
+    background thread while a leg runs; None fields when amdsmi is not usable
+    on the host (a reading, not part of the measurement)."""
+
+    def __init__(self, device_index=0):
+        self.handle = None
+        self.samples = []
+        self._stop = threading.Event()
+        self._thread = None
+        try:
+            import amdsmi
+            import torch
+
+            amdsmi.amdsmi_init()
+            self._amdsmi = amdsmi
+            handles = amdsmi.amdsmi_get_processor_handles()
+            props = torch.cuda.get_device_properties(device_index)
+            bus = getattr(props, "pci_bus_id", None)
+            for h in handles:
+                bdf = amdsmi.amdsmi_get_gpu_device_bdf(h)
+                if bus is None or int(bdf.split(":")[1], 16) == int(bus):
+                    self.handle = h
+                    break
+            if self.handle is None and len(handles) == 1:
+                self.handle = handles[0]
+        except Exception as exc:  # noqa: BLE001 - best-effort reading
+            self.error = f"{type(exc).__name__}: {exc}"[:200]
+
+    def _read(self):
+        info = self._amdsmi.amdsmi_get_clock_info(self.handle, self._amdsmi.AmdSmiClkType.GFX)
+        return float(info["clk"])
+
+    def _run(self):
+        while not self._stop.is_set():
+            try:
+                self.samples.append(self._read())
+            except Exception as exc:  # noqa: BLE001
+                self.error = f"{type(exc).__name__}: {exc}"[:200]
+                return
+            time.sleep(0.002)
+
+    def __enter__(self):
+        self.samples = []
+        self._stop.clear()
+        if self.handle is not None:
+            self._thread = threading.Thread(target=self._run, daemon=True)
+            self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        if self._thread is not None:
+            self._thread.join()
+            self._thread = None
+        return False
+
+    def summary(self):
+        if not self.samples:
+            return {"sclk_mhz_median": None, "sclk_samples": 0,
+                    "sclk_note": getattr(self, "error", "amdsmi not available")}
+        return {"sclk_mhz_median": median(self.samples), "sclk_mhz_min": min(self.samples),
+                "sclk_mhz_max": max(self.samples), "sclk_samples": len(self.samples)}
+
+
 PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_256x256_bf16_uniform.md"
-
-
 FP8_PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_fp8_cfg5.md"
 
 
-def recorded_traffic(mode, workload, block_m, block_n):
+def recorded_traffic(mode, workload, kernel_tile):
     """HBM bytes per launch from a committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
     (calibrated against a plain copy), when one covers this configuration; else None."""
-    if workload == "uniform" and (block_m, block_n) == (256, 256):
+    if workload == "uniform" and kernel_tile == (256, 256):
         path, key = PROFILE_SUMMARY, f"traffic_bytes_per_launch_{mode}:"
-    elif workload == "fp8" and (block_m, block_n) in ((256, 256), (256, 128), (192, 128)):
-        path, key = FP8_PROFILE_SUMMARY, f"traffic_bytes_per_launch_fp8_{block_m}x{block_n}_{mode}:"
+    elif workload == "fp8" and kernel_tile in ((256, 256), (256, 128), (192, 128)):
+        path, key = FP8_PROFILE_SUMMARY, f"traffic_bytes_per_launch_fp8_{kernel_tile[0]}x{kernel_tile[1]}_{mode}:"
     else:
         return None
     if not path.exists():
@@ -108,12 +210,7 @@ def recorded_traffic(mode, workload, block_m, block_n):
     return None
 
 
-def median(xs):
-    ys = sorted(xs)
-    return ys[len(ys) // 2] if ys else float("nan")
-
-
-def expert_mlp_summary(dev, steps: int = 10):
+def expert_mlp_summary(dev, steps: int = 20):
     """The benchmark expert-MLP config (8192 tokens top-2 of 16, H 2048, SwiGLU
     F 4096): whole forward (layout, gather, up GEMM + SwiGLU, down GEMM,
     combine) and each launch alone, from HIP events on the current stream."""
@@ -127,7 +224,7 @@ def expert_mlp_summary(dev, steps: int = 10):
     case.w_gate = case.w_up = None
     fwd = lambda: mlp.expert_mlp_forward(case.x, case.topk_idx, case.topk_weight, w1, case.w2,
                                          "swiglu")
-    event_times_ms(fwd, 30)  # ~30 ms of work: the card back at its steady clock after the set-up
+    settle_clock(fwd)
     t_fwd = median(event_times_ms(fwd, steps))
     lay = mlp.dispatch_layout(case.topk_idx, case.experts)
     xp = mlp.permute_tokens(case.x, lay)
@@ -161,10 +258,10 @@ def expert_mlp_summary(dev, steps: int = 10):
     return out
 
 
-def fp8_summary(dev, steps: int = 20):
+def fp8_summary(dev, steps: int = 40):
     """The benchmark fp8 config (E=64, M=24576, K=2048, N=1408, e4m3 with
     per-token x per-channel scales, bf16 out), HBM-bound by its algorithmic
-    bytes: each tile shape and schedule, kernel time from HIP events."""
+    bytes: each kernel tile and schedule, kernel time from HIP events."""
     import grouped_gemm as gg
     import workloads
 
@@ -177,21 +274,22 @@ def fp8_summary(dev, steps: int = 20):
     out = {"config": f"E={case.num_experts}, M={case.m}, K={case.k}, N={case.n}, e4m3 in, bf16 out",
            "algorithmic_bytes": t_bytes, "t_bound_us": round(max(t_flop_bound, t_hbm_bound) * 1e6, 2),
            "runs": {}}
-    out["default_tile"] = "{}x{}".format(*gg._default_fp8_blocks(case.m, case.num_experts))
+    out["default_tile"] = "{}x{}".format(*gg._default_fp8_kernel_tile(case.m, case.num_experts))
     best = None
-    for bm, bn in ((256, 256), (256, 128), (192, 128), (128, 128)):
+    for tile in ((256, 256), (256, 128), (192, 128), (128, 128)):
         for mode in ("striped", "atomic"):
-            fn = lambda: gg.persistent_grouped_gemm(case.a, b_kn, offs, block_m=bm, block_n=bn,
+            fn = lambda: gg.persistent_grouped_gemm(case.a, b_kn, offs, kernel_tile=tile,
                                                     use_atomic_queue=mode == "atomic",
                                                     a_scale=case.a_scale, b_scale=case.b_scale)
-            event_times_ms(fn, 100)
+            settle_clock(fn)
             t = median(event_times_ms(fn, steps))
             r = {"kernel_ms_median": round(t, 4),
                  "tflops": round(case.flops / (t * 1e-3) / 1e12, 1),
                  "hbm_gbps_at_algorithmic_bytes": round(t_bytes / (t * 1e-3) / 1e9, 1)}
-            out["runs"][f"{bm}x{bn}_{mode}"] = r
+            name = f"{tile[0]}x{tile[1]}_{mode}"
+            out["runs"][name] = r
             if best is None or t < best[1]:
-                best = (f"{bm}x{bn}_{mode}", t)
+                best = (name, t)
     out["best"] = best[0]
     out["best_frac_of_hbm_roofline"] = round(t_hbm_bound * 1e3 / best[1], 4)
     out["best_pct_fp8_peak"] = round(100 * case.flops / (best[1] * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 2)
@@ -253,48 +351,106 @@ def overlap_summary(case, offs, dev, iters: int = 60):
     return out
 
 
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(case, budget_s):
-    """The oracle's per-expert fp32 loop on the host cores, on a sample of experts."""
-    import numpy as np
-    from threadpoolctl import threadpool_info
+    """The reference's comparison loop, a per-expert torch matmul over each
+    expert's rows (src/triton_grouped_gemm.py:446-457, restated as
+    grouped_gemm.reference_grouped_gemm), on the host's cores in fp32: the
+    CPU-plumbing config (E=8, 128 tokens/expert, K=512, N=1024; >= 20 timed
+    iterations, median) and the metric's config with its bf16 inputs upcast
+    to fp32 (>= 3 timed iterations, median).  Threads: torch's default, which
+    follows OMP_NUM_THREADS (the GPU box's CPU share)."""
+    import torch
 
-    from oracle import grouped_gemm_oracle as orc
+    import grouped_gemm as gg
+    import workloads
 
-    a = case.a.float().cpu().numpy()
-    b = case.b.float().cpu().numpy()
-    offs = orc.expert_offsets_from_recv_counts(case.counts.numpy())
-    nonempty = [e for e in range(case.num_experts) if offs[e + 1] > offs[e]]
-    flops = 0
-    calls = 0
-    t0 = time.perf_counter()
-    out = np.empty((a.shape[0], b.shape[2]), np.float32)
-    # Cycle through the experts' slice GEMMs until the time budget is spent
-    # (at least one full pass over the workload).
-    while time.perf_counter() - t0 < budget_s or calls < len(nonempty):
-        e = nonempty[calls % len(nonempty)]
-        s, t = int(offs[e]), int(offs[e + 1])
-        orc.grouped_gemm(a[s:t], b[e:e + 1], [0, t - s], out=out[s:t])
-        flops += 2 * (t - s) * case.k * case.n
-        calls += 1
-    dt = time.perf_counter() - t0
-    threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    threads = torch.get_num_threads()
+
+    def timed(a, b, offs, min_iters, budget):
+        gg.reference_grouped_gemm(a, b, offs)  # warm-up (allocator, thread pool)
+        ts = []
+        t_end = time.perf_counter() + budget
+        while len(ts) < min_iters or time.perf_counter() < t_end:
+            t0 = time.perf_counter()
+            gg.reference_grouped_gemm(a, b, offs)
+            ts.append(time.perf_counter() - t0)
+        return ts
+
+    small = workloads.make_case("cpu_plumbing", device="cpu", dtype=torch.float32)
+    small_offs = gg.expert_offsets_from_recv_counts(small.counts)
+    ts_small = timed(small.a, small.b, small_offs, 20, 0.2 * budget_s)
+    a32 = case.a.float().cpu()
+    b32 = case.b.float().cpu()
+    offs = gg.expert_offsets_from_recv_counts(case.counts)
+    ts_big = timed(a32, b32, offs, 3, 0.6 * budget_s)
+    t_big = median(ts_big)
+    t_small = median(ts_small)
     return {
-        "value": round(flops / dt / 1e12, 5),
+        "value": round(case.flops / t_big / 1e12, 5),
         "unit": "TFLOP/s",
         "cores": int(threads),
         "kind": "port",
-        "sample": f"{calls} per-expert slice GEMMs cycling over the {len(nonempty)} experts of "
-                  f"the {case.name} workload ({flops / 1e9:.1f} GFLOP, fp32 numpy loop, {dt:.1f} s)",
+        "sample": f"{case.name} config (E={case.num_experts}, M={case.m}, K={case.k}, N={case.n}) with "
+                  f"its bf16 inputs upcast to fp32: per-expert torch matmul loop, median of "
+                  f"{len(ts_big)} iterations of {t_big * 1e3:.1f} ms",
+        "cpu_plumbing": {"config": f"E={small.num_experts}, M={small.m}, K={small.k}, N={small.n}, fp32",
+                         "ms_median": round(t_small * 1e3, 4), "iterations": len(ts_small),
+                         "tflops": round(small.flops / t_small / 1e12, 5)},
+        "threads": int(threads),
         "host_cpus": os.cpu_count(),
-        "cpu_model": platform.processor() or platform.machine(),
+        "cpu_model": _cpu_model(),
+        "torch_version": torch.__version__,
     }
+
+
+def _kernel_tile_arg(text):
+    if text is None:
+        return None
+    m, n = text.lower().split("x")
+    return int(m), int(n)
+
+
+def run_protocol(step, args, flops):
+    """Warmup, clock settling, the timed steps (wall clock) and the event
+    pass; returns the timing fields of the result line."""
+    import torch
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    settle = {"settle_launches": 0, "settle_ms": 0.0} if args.no_settle else settle_clock(step)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    out = {"wall_s": wall, **settle}
+    if args.profile_only:
+        return out
+    sampler = ClockSampler(torch.cuda.current_device())
+    with sampler:
+        kernel_ms = event_times_ms(step, max(args.steps, 50))
+    out.update(kernel_ms=kernel_ms, clock=sampler.summary())
+    return out
 
 
 def secondary_main(args, dev):
     """--workload expert_mlp | fp8: time one step of that config (the same
-    warmup / timed-steps / event protocol as the headline) and print its line."""
-    import torch
-
+    warmup / settle / timed-steps / event protocol as the headline) and print
+    its line."""
     import expert_mlp as mlp
     import grouped_gemm as gg
     import workloads
@@ -308,7 +464,7 @@ def secondary_main(args, dev):
                                               use_atomic_queue=args.mode == "atomic")
         flops, nbytes, bound, peak, dtype = case.flops, None, "mfma", PEAK_BF16_TFLOPS, "bf16"
         metric = "expert-MLP forward TFLOP/s (SwiGLU, T=8192 top-2 of 16, H2048 F4096)"
-        config_blocks = (256, 256)
+        tile = (256, 256)
         kernel = "grouped_gemm_kernel<256,256,32,4,8,Bf16,2> (up, SwiGLU) and <256,256,32,4,8,Bf16,0> (down)"
         config = {"workload": f"expert_mlp: T={case.tokens}, top-{case.top_k} of E={case.experts}, "
                               f"H={case.hidden}, F={case.ffn}, SwiGLU", "mode": args.mode}
@@ -316,55 +472,43 @@ def secondary_main(args, dev):
         case = workloads.make_fp8_case(device=dev)
         offs = gg.expert_offsets_from_recv_counts(case.counts, device=dev)
         b_kn = case.b_nk.transpose(1, 2)
-        # The library's default fp8 tile (256x256 here) unless another tile is named.
-        bm, bn = ((gg._default_fp8_blocks(case.m, case.num_experts))
-                  if (args.block_m, args.block_n) == (256, 256) else (args.block_m, args.block_n))
+        tile = _kernel_tile_arg(args.kernel_tile) or gg._default_fp8_kernel_tile(case.m, case.num_experts)
         step = lambda: gg.persistent_grouped_gemm(case.a, b_kn, offs, num_sms=args.num_sms,
-                                                  block_m=bm, block_n=bn,
+                                                  block_m=args.block_m, block_n=args.block_n,
+                                                  kernel_tile=tile,
                                                   use_atomic_queue=args.mode == "atomic",
                                                   a_scale=case.a_scale, b_scale=case.b_scale)
         flops, nbytes, bound, peak, dtype = case.flops, case.algorithmic_bytes(), "hbm", PEAK_HBM_GBPS, "fp8_e4m3"
         metric = "fp8 grouped GEMM TFLOP/s, E=64 M=24576 K2048 N1408 (per-token x per-channel scales)"
         config = {"workload": f"fp8: E={case.num_experts}, M={case.m}, K={case.k}, N={case.n}",
-                  "mode": args.mode, "block_m": bm, "block_n": bn}
-        config_blocks = (bm, bn)
-        stages = 2 if (bm, bn) == (256, 256) else (4 if bm == 128 else 3)
-        kernel = f"grouped_gemm_kernel<{bm},{bn},128,{stages},8,Fp8,0>"
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+                  "mode": args.mode, "kernel_tile": f"{tile[0]}x{tile[1]}"}
+        stages = 2 if tile == (256, 256) else (4 if tile[0] == 128 else 3)
+        kernel = f"grouped_gemm_kernel<{tile[0]},{tile[1]},128,{stages},8,Fp8,0>"
+    r = run_protocol(step, args, flops)
+    wall = r["wall_s"]
     if args.profile_only:
         print(json.dumps({"profile_only": True, "workload": args.workload,
-                          "ms_per_step": wall / args.steps * 1e3}))
+                          "ms_per_step": wall / args.steps * 1e3,
+                          "settle_launches": r["settle_launches"]}))
         return
-    # Per-launch times in a pass of their own (event records stay out of the wall clock).
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    for i in range(args.steps):
-        starts[i].record()
-        step()
-        ends[i].record()
-    torch.cuda.synchronize()
-    k_mean = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / args.steps
+    k_med = median(r["kernel_ms"])
     value = flops * args.steps / wall / 1e12
     if bound == "hbm":
-        achieved, unit = nbytes / (k_mean * 1e-3) / 1e9, "GB/s"
+        achieved, unit = nbytes / (k_med * 1e-3) / 1e9, "GB/s"
     else:
-        achieved, unit = flops / (k_mean * 1e-3) / 1e12, "TFLOP/s"
+        achieved, unit = flops / (k_med * 1e-3) / 1e12, "TFLOP/s"
     print(json.dumps({
         "metric": metric, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
         "data": "synthetic (benchmark recipe, random init)", "config": config,
-        "kernel_ms_mean": round(k_mean, 5),
+        "settle_launches": r["settle_launches"], "settle_ms": r["settle_ms"],
+        "kernel_ms_median": round(k_med, 5), "kernel_ms_min": round(min(r["kernel_ms"]), 5),
+        "kernel_ms_mean": round(sum(r["kernel_ms"]) / len(r["kernel_ms"]), 5),
+        "clock": r["clock"],
         "roofline": {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
                      "frac": round(achieved / peak, 4),
-                     "traffic": recorded_traffic(args.mode, args.workload, *config_blocks),
+                     "traffic": recorded_traffic(args.mode, args.workload, tile),
                      "kernel": kernel,
                      "algorithmic_flops_per_step": flops, "algorithmic_bytes_per_step": nbytes},
     }), flush=True)
@@ -374,7 +518,8 @@ def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the grouped GEMM shards by expert across GPUs; one GPU's share is what runs here).", file=sys.stderr)
+              "(the grouped GEMM shards by expert across GPUs; one GPU's share is what runs here).",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -399,38 +544,25 @@ def main():
     case = workloads.make_case(args.workload, device=dev, dtype=torch.bfloat16)
     offs = gg.expert_offsets_from_recv_counts(case.counts, device=dev)
     atomic = args.mode == "atomic"
+    kernel_tile = _kernel_tile_arg(args.kernel_tile) or gg._default_kernel_tile(case.m, case.num_experts)
     kw = dict(num_sms=args.num_sms, block_m=args.block_m, block_n=args.block_n,
-              use_atomic_queue=atomic)
+              use_atomic_queue=atomic, kernel_tile=kernel_tile)
 
     def step():
         return gg.persistent_grouped_gemm(case.a, case.b, offs, **kw)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    if args.profile_only:
-        print(json.dumps({"profile_only": True, "ms_per_step": wall / args.steps * 1e3}))
-        return
-    # Per-launch kernel times: the same steps again with HIP events around each launch, in a pass
-    # of their own (event records are stream commands of their own, kept out of the wall clock).
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    for i in range(args.steps):
-        starts[i].record()
-        step()
-        ends[i].record()
-    torch.cuda.synchronize()
-    kernel_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-
     flops = case.flops
+    r = run_protocol(step, args, flops)
+    wall = r["wall_s"]
+    if args.profile_only:
+        print(json.dumps({"profile_only": True, "ms_per_step": wall / args.steps * 1e3,
+                          "settle_launches": r["settle_launches"]}))
+        return
+    kernel_ms = r["kernel_ms"]
     value = flops * args.steps / wall / 1e12
+    k_med = median(kernel_ms)
     k_mean = sum(kernel_ms) / len(kernel_ms)
-    achieved = flops / (k_mean * 1e-3) / 1e12
+    achieved = flops / (k_med * 1e-3) / 1e12
 
     # Correctness of the timed configuration against an fp32 torch loop.
     c = step()
@@ -441,8 +573,19 @@ def main():
 
     extra = {}
     if not args.no_compare:
-        # The other benchmark configs first, while the card is at its steady clock (the legs below
-        # load it for seconds; its clock sags under sustained load).
+        # The reference's own call (its benchmark passes block_m = block_n = 128 explicitly,
+        # src/bench_triton_grouped_gemm.py:19-20, :83-91) against the library default.
+        legs = {}
+        for name, extra_kw in (("default_call", {}),
+                               ("explicit_128x128", dict(block_m=128, block_n=128)),
+                               ("kernel_tile_128x128", dict(kernel_tile=(128, 128)))):
+            fn = lambda: gg.persistent_grouped_gemm(case.a, case.b, offs, use_atomic_queue=atomic,
+                                                    **extra_kw)
+            settle_clock(fn)
+            t = median(event_times_ms(fn, 50))
+            legs[name] = {"kernel_ms_median": round(t, 5),
+                          "tflops": round(flops / (t * 1e-3) / 1e12, 1)}
+        extra["reference_calls"] = legs
         extra["expert_mlp"] = expert_mlp_summary(dev)
         extra["fp8"] = fp8_summary(dev)
         sched = {}
@@ -451,10 +594,10 @@ def main():
             o = gg.expert_offsets_from_recv_counts(cs.counts, device=dev)
             for mode in ("striped", "atomic"):
                 fn = lambda: gg.persistent_grouped_gemm(
-                    cs.a, cs.b, o, num_sms=args.num_sms, block_m=args.block_m,
-                    block_n=args.block_n, use_atomic_queue=(mode == "atomic"))
-                event_times_ms(fn, 100)  # steady clock before timing each schedule
-                t = event_times_ms(fn, 40)
+                    cs.a, cs.b, o, num_sms=args.num_sms, kernel_tile=kernel_tile,
+                    use_atomic_queue=(mode == "atomic"))
+                settle_clock(fn)
+                t = event_times_ms(fn, 50)
                 sched[f"{wl}_{mode}"] = {
                     "kernel_ms_median": round(median(t), 4), "kernel_ms_min": round(min(t), 4),
                     "tflops": round(cs.flops / (median(t) * 1e-3) / 1e12, 1)}
@@ -463,25 +606,25 @@ def main():
         extra["schedules"] = sched
         # The reference API's per-expert torch loop on the GPU (hipBLASLt GEMMs).
         loop = lambda: gg.reference_grouped_gemm(case.a, case.b, offs)
-        event_times_ms(loop, 2)
-        tl = event_times_ms(loop, 5)
+        event_times_ms(loop, 3)
+        tl = event_times_ms(loop, 10)
         extra["torch_loop_gpu_ms_median"] = round(median(tl), 4)
         extra["torch_loop_gpu_tflops"] = round(flops / (median(tl) * 1e-3) / 1e12, 1)
         counts_l = case.counts.tolist()
         if len(set(counts_l)) == 1 and counts_l[0] > 0:
             # Equal counts make the problem one batched GEMM: the vendor library's batched
             # kernel (torch.bmm -> hipBLASLt) on the same operands, for reference.
-            e, c = len(counts_l), counts_l[0]
-            a3 = case.a[: e * c].view(e, c, case.k)
+            e, c_e = len(counts_l), counts_l[0]
+            a3 = case.a[: e * c_e].view(e, c_e, case.k)
             bmm = lambda: torch.bmm(a3, case.b)
-            event_times_ms(bmm, 50)
-            tb = event_times_ms(bmm, 40)
+            settle_clock(bmm)
+            tb = event_times_ms(bmm, 50)
             extra["hipblaslt_bmm_ms_median"] = round(median(tb), 4)
             extra["hipblaslt_bmm_tflops"] = round(flops / (median(tb) * 1e-3) / 1e12, 1)
         extra["overlap"] = overlap_summary(case, offs, dev)
         # Cache-cold launches: a 512 MiB write evicts L2 and the 256 MB MALL.
         scratch = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
-        cold = event_times_ms(step, 10, flush=lambda: scratch.fill_(1.0))
+        cold = event_times_ms(step, 20, flush=lambda: scratch.fill_(1.0))
         extra["cold_kernel_ms_median"] = round(median(cold), 4)
         extra["cold_tflops"] = round(flops / (median(cold) * 1e-3) / 1e12, 1)
         del scratch
@@ -506,12 +649,19 @@ def main():
             "mode": args.mode,
             "block_m": args.block_m,
             "block_n": args.block_n,
+            "kernel_tile": f"{kernel_tile[0]}x{kernel_tile[1]}",
             "num_sms": args.num_sms or "all CUs",
             "queue": "device",
         },
+        "settle_launches": r["settle_launches"],
+        "settle_ms": r["settle_ms"],
+        "settled": r.get("settled"),
         "pct_bf16_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
-        "kernel_ms_mean": round(k_mean, 5),
+        "event_launches": len(kernel_ms),
+        "kernel_ms_median": round(k_med, 5),
         "kernel_ms_min": round(min(kernel_ms), 5),
+        "kernel_ms_mean": round(k_mean, 5),
+        "clock": r["clock"],
         "max_abs_diff_vs_fp32": round(max_abs, 6),
         "tolerance": round(tolerance, 6),
         "roofline": {
@@ -520,13 +670,14 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": recorded_traffic(args.mode, args.workload, args.block_m, args.block_n),
+            "achieved_from": "median HIP-event launch time",
+            "traffic": recorded_traffic(args.mode, args.workload, kernel_tile),
             "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), "
                               "profiles/grouped_gemm_256x256_bf16_uniform.md",
-            "kernel": KERNEL_NAME if (args.block_m, args.block_n) == (256, 256) else "grouped_gemm_kernel",
+            "kernel": KERNEL_NAME if kernel_tile == (256, 256) else "grouped_gemm_kernel",
             "algorithmic_flops_per_launch": flops,
             "algorithmic_bytes_per_launch": case.algorithmic_bytes(),
-            "hbm_gbps_at_algorithmic_bytes": round(case.algorithmic_bytes() / (k_mean * 1e-3) / 1e9, 1),
+            "hbm_gbps_at_algorithmic_bytes": round(case.algorithmic_bytes() / (k_med * 1e-3) / 1e9, 1),
         },
         "cpu_baseline": cpu,
         **extra,

@@ -36,6 +36,9 @@
  *   mgg_combine_rows               -> out[valid] = grouped_out[inv_perm] and
  *                                     out += y * gate over the top-k slots
  *                                     (src/train_moe_baseline.py:245-246, :340-341)
+ *   mgg_debug_set_dequeue_counter  -> no counterpart: a test hook (the
+ *                                     reference zeroes its counter on the
+ *                                     host before each launch, :379-386)
  */
 #ifndef MGG_H_
 #define MGG_H_
@@ -133,31 +136,42 @@ int mgg_build_work_queue_host(const int64_t* expert_offsets, int64_t num_experts
  * num_workers persistent workgroups are launched (<= 0 means one per CU).
  * use_atomic_queue = 0: worker w takes items w, w+G, w+2G, ... (workers are
  * numbered so that each XCD owns a contiguous slice of every round).
- * use_atomic_queue = 1: workers take the next item with atomicAdd on a global
- * int32 counter owned by the library, one per (device, stream), which starts
- * every launch at zero and is returned to zero by the last worker to exit.
- * If work_counter is non-null (device int32) it receives that counter's final
- * value, num_work + G (each worker over-fetches once), which is the value the
- * reference leaves in its work_counter (:379-416); with an empty queue it is
- * left untouched, as there.  Calls on one stream are ordered; calls on
+ * use_atomic_queue = 1: workers take the next item with an atomic add on a
+ * 64-bit counter word owned by the library: one per (device, stream) for
+ * direct launches, and one of its own for every launch captured into a HIP
+ * graph (so graph replays never share a word with other launches).  The
+ * words live in a file-scope device array (no allocation; at most 4096 per
+ * device).  Each launch tags the word with a fresh epoch and claims whatever
+ * it finds there, so a word left dirty by a launch that did not finish never
+ * drops or repeats tiles; the launch's last ticket returns it to zero.
+ * If work_counter is non-null (device int32) it receives W + G, the value
+ * the reference's counter ends at (:379-416: each worker over-fetches once),
+ * where W is the queue length of the report tile, report_block_m x
+ * report_block_n (<= 0: block_m x block_n): the tile the caller asked for
+ * when the library computes with another.  With an empty queue it is left
+ * untouched, as there.  Calls on one stream are ordered; calls on
  * different streams use different counters.
  *
- * If the queue is empty, C is zero-filled.  Rows of C not covered by any
- * expert range are left unwritten.  Supported: dtype BF16/FP16,
+ * If the queue is empty, C is zero-filled; with K == 0 the covered rows are
+ * zeros (A and B and their strides are not read).  Rows of C not covered by
+ * any expert range are left unwritten.  Supported: dtype BF16/FP16,
  * block_m, block_n in {64, 128, 256}, K % 8 == 0, N % 8 == 0, strides
  * multiples of 8 elements, 16-byte aligned base pointers, E <= 2048 when the
  * queue is derived on the device.
+ * (ABI version 4 added report_block_m, report_block_n.)
  */
 int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
                      const int32_t* expert_offsets, int64_t m_size, int64_t k_size, int64_t n_size,
                      int64_t num_experts, int64_t lda, int64_t ldb_e, int64_t ldb_k, int64_t ldc,
                      const int32_t* work_expert, const int32_t* work_tile_m,
                      const int32_t* work_tile_n, int64_t num_work, int block_m, int block_n,
-                     int num_workers, int use_atomic_queue, int32_t* work_counter, void* stream);
+                     int num_workers, int use_atomic_queue, int32_t* work_counter,
+                     int report_block_m, int report_block_n, void* stream);
 
 /*
- * mgg_grouped_gemm with a fused element-wise epilogue and the queue always
- * derived on the device.  Same arguments and semantics otherwise.
+ * mgg_grouped_gemm with a fused element-wise epilogue.  Same arguments and
+ * semantics otherwise (the queue is derived on the device when num_work < 0,
+ * or read from work_expert/work_tile_m/work_tile_n, e.g. above 2048 experts).
  *   MGG_EPI_GELU:   C[r, n] = gelu(sum_k A[r, k] B[e, k, n]) (fp32, then rounded).
  *   MGG_EPI_SWIGLU: B's N columns hold gate and up projections interleaved in
  *                   groups of 64: columns 64q .. 64q+31 are gate outputs
@@ -165,13 +179,17 @@ int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
  *                   the same indices.  C has N/2 columns:
  *                   C[r, f] = silu(gate[r, f]) * up[r, f].  N % 64 == 0.
  * Fused epilogues are compiled for block_m == block_n in {128, 256}.
- * (Introduced with ABI version 2.)
+ * (Introduced with ABI version 2; version 4 added the queue and report-tile
+ * arguments.)
  */
 int mgg_grouped_gemm_ex(int dtype, int epilogue, const void* a, const void* b, void* c,
                         const int32_t* expert_offsets, int64_t m_size, int64_t k_size,
                         int64_t n_size, int64_t num_experts, int64_t lda, int64_t ldb_e,
-                        int64_t ldb_k, int64_t ldc, int block_m, int block_n, int num_workers,
-                        int use_atomic_queue, int32_t* work_counter, void* stream);
+                        int64_t ldb_k, int64_t ldc, const int32_t* work_expert,
+                        const int32_t* work_tile_m, const int32_t* work_tile_n, int64_t num_work,
+                        int block_m, int block_n, int num_workers, int use_atomic_queue,
+                        int32_t* work_counter, int report_block_m, int report_block_n,
+                        void* stream);
 
 /*
  * fp8 grouped GEMM with per-token and per-channel scales:
@@ -182,18 +200,29 @@ int mgg_grouped_gemm_ex(int dtype, int epilogue, const void* a, const void* b, v
  *                 linear layer's weight), expert stride ldb_e, row stride ldb_n
  *   a_scale [M], b_scale [E, N] (row stride N): fp32 on the device
  *   c  [M, N]     BF16, row stride ldc
- * Queue, schedules, work_counter and empty-queue behaviour as in
- * mgg_grouped_gemm (queue derived on the device).  Tiles 256x256, 256x128,
+ * Queue (derived on the device, or prebuilt), schedules, work_counter and
+ * empty-queue behaviour as in mgg_grouped_gemm.  Tiles 256x256, 256x128,
  * 192x128 and 128x128; K, lda, ldb_n, ldb_e multiples of 16; N, ldc
  * multiples of 8.
- * (Introduced with ABI version 2.)
+ * (Introduced with ABI version 2; version 4 added the queue and report-tile
+ * arguments.)
  */
 int mgg_grouped_gemm_fp8(const void* a, const void* b, void* c, const int32_t* expert_offsets,
                          const float* a_scale, const float* b_scale, int64_t m_size,
                          int64_t k_size, int64_t n_size, int64_t num_experts, int64_t lda,
-                         int64_t ldb_e, int64_t ldb_n, int64_t ldc, int block_m, int block_n,
-                         int num_workers, int use_atomic_queue, int32_t* work_counter,
-                         void* stream);
+                         int64_t ldb_e, int64_t ldb_n, int64_t ldc, const int32_t* work_expert,
+                         const int32_t* work_tile_m, const int32_t* work_tile_n,
+                         int64_t num_work, int block_m, int block_n, int num_workers,
+                         int use_atomic_queue, int32_t* work_counter, int report_block_m,
+                         int report_block_n, void* stream);
+
+/*
+ * Test hook, no counterpart in the reference: writes `value` into the atomic
+ * queue's counter word of direct launches on `stream` (current device), the
+ * state a launch that did not finish could leave behind, so tests can check
+ * that the next launch still computes every tile.  Enqueued on `stream`.
+ */
+int mgg_debug_set_dequeue_counter(uint64_t value, void* stream);
 
 /*
  * Dispatch layout of T tokens routed to top_k experts each (one GPU's share):

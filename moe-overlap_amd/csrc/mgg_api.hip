@@ -2,45 +2,94 @@
 // validation, library-owned dequeue counters, and the launches.  No C++
 // exception crosses this boundary; failures return a status code and leave a
 // message for mgg_last_error().
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "mgg.h"
 #include "mgg_internal.h"
 
 namespace mgg {
+
+// Dequeue counters of the atomic schedule: one 64-bit word per slot, in a
+// file-scope device array (each device holds its own copy for the life of
+// the process), so no entry point allocates memory.  A word holds (epoch <<
+// 32) | count; each launch carries a fresh epoch and claims whatever value
+// it finds (see first_ticket in mgg_gemm.hip), so a launch that did not run
+// to its end cannot leave a count that the next launch trusts.
+constexpr int kCounterSlots = 4096;
+__device__ __align__(256) unsigned long long counter_pool[kCounterSlots];
+
 namespace {
 
 thread_local std::string g_last_error;
 
-// Library-owned {counter, done} pairs, one per (device, stream).  Each lives
-// until the process ends; the GEMM kernel leaves both at zero when it exits.
-std::mutex g_counter_mutex;
-std::map<std::pair<int, hipStream_t>, int32_t*> g_counters;
+std::atomic<uint32_t> g_epoch{0};
 
-int counters_for(hipStream_t stream, int32_t** out) {
+uint32_t next_epoch() {
+  uint32_t e = ++g_epoch;
+  while (e == 0) e = ++g_epoch;  // 0 is the value a finished launch leaves
+  return e;
+}
+
+// Slots: launches on one (device, stream) share a slot (they run in stream
+// order); a launch captured into a graph gets a slot of its own for good, so
+// replays of the graph never share a word with direct launches on the
+// capture stream or with another captured launch.
+struct CounterSlots {
+  std::mutex mu;
+  std::map<std::pair<int, hipStream_t>, int> by_stream;
+  std::vector<unsigned long long*> base;  // per device: counter_pool's address there
+  std::vector<int> used;                  // per device: slots handed out
+};
+CounterSlots g_slots;
+
+int pool_base(int device, unsigned long long** out) {
+  if ((int)g_slots.base.size() <= device) {
+    g_slots.base.resize(device + 1, nullptr);
+    g_slots.used.resize(device + 1, 0);
+  }
+  if (g_slots.base[device] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(counter_pool));
+    if (err != hipSuccess) return hip_error(err, "hipGetSymbolAddress(counter_pool)");
+    g_slots.base[device] = static_cast<unsigned long long*>(ptr);
+  }
+  *out = g_slots.base[device];
+  return MGG_OK;
+}
+
+// The counter word for a launch on `stream` (current device).
+int counter_for(hipStream_t stream, unsigned long long** out) {
   int device = 0;
   hipError_t err = hipGetDevice(&device);
   if (err != hipSuccess) return hip_error(err, "hipGetDevice");
-  std::lock_guard<std::mutex> lock(g_counter_mutex);
-  auto key = std::make_pair(device, stream);
-  auto it = g_counters.find(key);
-  if (it != g_counters.end()) {
-    *out = it->second;
-    return MGG_OK;
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (stream != nullptr) {
+    err = hipStreamIsCapturing(stream, &capture);
+    if (err != hipSuccess) return hip_error(err, "hipStreamIsCapturing");
   }
-  int32_t* buf = nullptr;
-  err = hipMalloc(reinterpret_cast<void**>(&buf), 2 * sizeof(int32_t));
-  if (err != hipSuccess) return hip_error(err, "hipMalloc(dequeue counters)");
-  const int rc = launch_zero_i32(buf, 2, stream);
-  if (rc != MGG_OK) {
-    (void)hipFree(buf);
-    return rc;
+  std::lock_guard<std::mutex> lock(g_slots.mu);
+  unsigned long long* base = nullptr;
+  const int rc = pool_base(device, &base);
+  if (rc != MGG_OK) return rc;
+  const auto key = std::make_pair(device, stream);
+  if (capture == hipStreamCaptureStatusNone) {
+    auto it = g_slots.by_stream.find(key);
+    if (it != g_slots.by_stream.end()) {
+      *out = base + it->second;
+      return MGG_OK;
+    }
   }
-  g_counters.emplace(key, buf);
-  *out = buf;
+  if (g_slots.used[device] >= kCounterSlots)
+    return set_error(MGG_ERR_UNSUPPORTED,
+                     "atomic queue: more than 4096 streams and captured launches on one device");
+  const int slot = g_slots.used[device]++;
+  if (capture == hipStreamCaptureStatusNone) g_slots.by_stream.emplace(key, slot);
+  *out = base + slot;
   return MGG_OK;
 }
 
@@ -64,7 +113,7 @@ using mgg::set_error;
 
 extern "C" {
 
-int mgg_abi_version(void) { return 3; }
+int mgg_abi_version(void) { return 4; }
 
 const char* mgg_last_error(void) { return mgg::g_last_error.c_str(); }
 
@@ -177,7 +226,7 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
                       const int32_t* work_tile_m, const int32_t* work_tile_n, int64_t num_work,
                       const float* a_scale, const float* b_scale, int block_m, int block_n,
                       int num_workers, int use_atomic_queue, int32_t* work_counter,
-                      hipStream_t st) {
+                      int report_block_m, int report_block_n, hipStream_t st) {
   const bool fp8 = dtype == MGG_DTYPE_FP8_E4M3;
   const int base = dtype & ~MGG_B_KMAJOR;
   const bool kmajor = (dtype & MGG_B_KMAJOR) != 0;  // 16-bit B stored [E, N, K]
@@ -203,6 +252,13 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   if (m_size == 0 || n_size == 0) return MGG_OK;  // C has no elements
   if (k_size % 8 != 0 || n_size % 8 != 0)
     return set_error(MGG_ERR_UNSUPPORTED, "K and N must be multiples of 8");
+  // K == 0: nothing is read (every DMA is past its descriptor, so the tiles
+  // hold zeros); A's and B's strides are then unused.
+  if (k_size == 0) {
+    lda = 0;
+    ldb_k = b_rows_k ? 0 : n_size;
+    ldb_e = 0;
+  }
   if (fp8 && (k_size % 16 != 0 || lda % 16 != 0 || ldb_k % 16 != 0 || ldb_e % 16 != 0))
     return set_error(MGG_ERR_UNSUPPORTED, "fp8: K and the A/B strides must be multiples of 16");
   if (epilogue == MGG_EPI_SWIGLU && n_size % 64 != 0)
@@ -210,6 +266,8 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   const int64_t c_cols = epilogue == MGG_EPI_SWIGLU ? n_size / 2 : n_size;
   // ldb_k: stride between B's rows (K rows of N values; for fp8 and K-major
   // B, N rows of K values).
+  if (report_block_m <= 0) report_block_m = block_m;
+  if (report_block_n <= 0) report_block_n = block_n;
   if (lda < k_size || ldb_k < (b_rows_k ? k_size : n_size) || ldc < c_cols || ldb_e < 0)
     return set_error(MGG_ERR_INVALID, "leading dimensions smaller than the matrix extents");
   if (lda % 8 != 0 || ldb_k % 8 != 0 || ldb_e % 8 != 0 || ldc % 8 != 0)
@@ -277,12 +335,12 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   p.num_work = num_work >= 0 ? (int32_t)num_work : -1;
   p.atomic = use_atomic_queue ? 1 : 0;
   p.remap_xcd = 1;
+  p.report_bm = report_block_m;
+  p.report_bn = report_block_n;
   if (p.atomic) {
-    int32_t* counters = nullptr;
-    const int rc = counters_for(st, &counters);
+    const int rc = counter_for(st, &p.counter);
     if (rc != MGG_OK) return rc;
-    p.counter = counters;
-    p.done = counters + 1;
+    p.epoch = next_epoch();
     p.report = work_counter;
   }
   return launch_grouped_gemm(dtype, epilogue, block_m, block_n, p, workers, st);
@@ -298,41 +356,57 @@ int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
                      int64_t num_experts, int64_t lda, int64_t ldb_e, int64_t ldb_k, int64_t ldc,
                      const int32_t* work_expert, const int32_t* work_tile_m,
                      const int32_t* work_tile_n, int64_t num_work, int block_m, int block_n,
-                     int num_workers, int use_atomic_queue, int32_t* work_counter, void* stream) {
+                     int num_workers, int use_atomic_queue, int32_t* work_counter,
+                     int report_block_m, int report_block_n, void* stream) {
   mgg::clear_error();
   return mgg::grouped_gemm_impl(dtype, MGG_EPI_NONE, a, b, c, expert_offsets, m_size, k_size,
                                 n_size, num_experts, lda, ldb_e, ldb_k, ldc, work_expert,
                                 work_tile_m, work_tile_n, num_work, nullptr, nullptr, block_m,
                                 block_n, num_workers, use_atomic_queue, work_counter,
-                                static_cast<hipStream_t>(stream));
+                                report_block_m, report_block_n, static_cast<hipStream_t>(stream));
 }
 
 int mgg_grouped_gemm_ex(int dtype, int epilogue, const void* a, const void* b, void* c,
                         const int32_t* expert_offsets, int64_t m_size, int64_t k_size,
                         int64_t n_size, int64_t num_experts, int64_t lda, int64_t ldb_e,
-                        int64_t ldb_k, int64_t ldc, int block_m, int block_n, int num_workers,
-                        int use_atomic_queue, int32_t* work_counter, void* stream) {
+                        int64_t ldb_k, int64_t ldc, const int32_t* work_expert,
+                        const int32_t* work_tile_m, const int32_t* work_tile_n, int64_t num_work,
+                        int block_m, int block_n, int num_workers, int use_atomic_queue,
+                        int32_t* work_counter, int report_block_m, int report_block_n,
+                        void* stream) {
   mgg::clear_error();
   if (dtype == MGG_DTYPE_FP8_E4M3)
     return set_error(MGG_ERR_UNSUPPORTED, "fp8 goes through mgg_grouped_gemm_fp8");
   return mgg::grouped_gemm_impl(dtype, epilogue, a, b, c, expert_offsets, m_size, k_size, n_size,
-                                num_experts, lda, ldb_e, ldb_k, ldc, nullptr, nullptr, nullptr, -1,
-                                nullptr, nullptr, block_m, block_n, num_workers, use_atomic_queue,
-                                work_counter, static_cast<hipStream_t>(stream));
+                                num_experts, lda, ldb_e, ldb_k, ldc, work_expert, work_tile_m,
+                                work_tile_n, num_work, nullptr, nullptr, block_m, block_n,
+                                num_workers, use_atomic_queue, work_counter, report_block_m,
+                                report_block_n, static_cast<hipStream_t>(stream));
 }
 
 int mgg_grouped_gemm_fp8(const void* a, const void* b, void* c, const int32_t* expert_offsets,
                          const float* a_scale, const float* b_scale, int64_t m_size,
                          int64_t k_size, int64_t n_size, int64_t num_experts, int64_t lda,
-                         int64_t ldb_e, int64_t ldb_n, int64_t ldc, int block_m, int block_n,
-                         int num_workers, int use_atomic_queue, int32_t* work_counter,
-                         void* stream) {
+                         int64_t ldb_e, int64_t ldb_n, int64_t ldc, const int32_t* work_expert,
+                         const int32_t* work_tile_m, const int32_t* work_tile_n,
+                         int64_t num_work, int block_m, int block_n, int num_workers,
+                         int use_atomic_queue, int32_t* work_counter, int report_block_m,
+                         int report_block_n, void* stream) {
   mgg::clear_error();
   return mgg::grouped_gemm_impl(MGG_DTYPE_FP8_E4M3, MGG_EPI_NONE, a, b, c, expert_offsets, m_size,
-                                k_size, n_size, num_experts, lda, ldb_e, ldb_n, ldc, nullptr,
-                                nullptr, nullptr, -1, a_scale, b_scale, block_m, block_n,
-                                num_workers, use_atomic_queue, work_counter,
-                                static_cast<hipStream_t>(stream));
+                                k_size, n_size, num_experts, lda, ldb_e, ldb_n, ldc, work_expert,
+                                work_tile_m, work_tile_n, num_work, a_scale, b_scale, block_m,
+                                block_n, num_workers, use_atomic_queue, work_counter,
+                                report_block_m, report_block_n, static_cast<hipStream_t>(stream));
+}
+
+int mgg_debug_set_dequeue_counter(uint64_t value, void* stream) {
+  mgg::clear_error();
+  unsigned long long* word = nullptr;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const int rc = mgg::counter_for(st, &word);
+  if (rc != MGG_OK) return rc;
+  return mgg::launch_fill_u64(word, 1, (unsigned long long)value, st);
 }
 
 int64_t mgg_dispatch_layout_workspace_bytes(int64_t num_tokens, int top_k, int64_t num_experts) {

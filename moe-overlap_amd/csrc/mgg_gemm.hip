@@ -169,25 +169,31 @@ __device__ __forceinline__ float silu_mul(float gate, float up) {  // silu(gate)
 // Per-expert tile prefix of the derived queue, built in LDS by the whole
 // workgroup: prefix[e] = sum_{j<e} ceil(max(off[j+1]-off[j],0)/BM) * n_tiles.
 // Returns the queue length W = prefix[E].  Same counts as
-// src/triton_grouped_gemm.py:253-271.
+// src/triton_grouped_gemm.py:253-271.  With `rep_tiles` set, *w_report gets
+// the queue length of the report tile (p.report_bm x p.report_bn, rep_tiles
+// column tiles) from the same pass over the offsets; else it is W.
 template <int BM, int NT>
 __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_prefix,
-                                 int32_t* s_offs, int32_t* s_scan) {
+                                 int32_t* s_offs, int32_t* s_scan, int rep_tiles,
+                                 int32_t* w_report) {
   const int tid = threadIdx.x;
   const int E = p.num_experts;
   const int per = (E + NT - 1) / NT;
   const int e0 = tid * per;
   int32_t local = 0;
+  int64_t rep_local = 0;
   for (int i = 0; i < per; ++i) {
     const int e = e0 + i;
     if (e < E) {
       const int64_t cnt = (int64_t)p.offsets[e + 1] - (int64_t)p.offsets[e];
       const int64_t tiles = cnt > 0 ? ((cnt + BM - 1) / BM) * (int64_t)n_tiles : 0;
       local += (int32_t)tiles;
+      if (rep_tiles > 0 && cnt > 0) rep_local += ((cnt + p.report_bm - 1) / p.report_bm) * (int64_t)rep_tiles;
     }
   }
   // Inclusive scan of the NT per-thread sums: within each wave by lane
-  // shuffles, then across the NT/64 wave totals (one barrier).
+  // shuffles, then across the NT/64 wave totals (one barrier).  The report
+  // count is a plain sum (wave totals in s_scan[NT/64 ..]).
   const int lane = tid & 63;
   const int wave = tid >> 6;
   int32_t incl = local;
@@ -196,8 +202,19 @@ __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_pr
     const int32_t y = __shfl_up(incl, d);
     if (lane >= d) incl += y;
   }
+  if (rep_tiles > 0) {
+    int32_t r = (int32_t)rep_local;  // the reference's int32 counter wraps the same way
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) r += __shfl_xor(r, d);
+    if (lane == 0) s_scan[NT / 64 + wave] = r;
+  }
   if (lane == 63) s_scan[wave] = incl;
   __syncthreads();
+  if (rep_tiles > 0) {
+    int32_t r = 0;
+    for (int v = 0; v < NT / 64; ++v) r += s_scan[NT / 64 + v];
+    *w_report = r;
+  }
   for (int v = 0; v < wave; ++v) incl += s_scan[v];
   int32_t base = incl - local;
   for (int i = 0; i < per; ++i) {
@@ -214,7 +231,61 @@ __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_pr
     if (s_offs != nullptr) s_offs[E] = p.offsets[E];
   }
   __syncthreads();
-  return s_prefix[E];
+  const int32_t W = s_prefix[E];
+  if (rep_tiles <= 0) *w_report = W;
+  return W;
+}
+
+// sum_e ceil(max(off[e+1]-off[e], 0) / bm) * n_tiles over every expert (any
+// count), wrapped to int32 as the reference's int32 counter wraps; the whole
+// workgroup calls it.
+template <int NT>
+__device__ int32_t queue_length(const GemmParams& p, int bm, int n_tiles, int32_t* s_scan) {
+  const int tid = threadIdx.x;
+  int64_t local = 0;
+  for (int e = tid; e < p.num_experts; e += NT) {
+    const int64_t cnt = (int64_t)p.offsets[e + 1] - (int64_t)p.offsets[e];
+    if (cnt > 0) local += ((cnt + bm - 1) / bm) * (int64_t)n_tiles;
+  }
+  int32_t r = (int32_t)local;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) r += __shfl_xor(r, d);
+  __syncthreads();  // s_scan may hold another reduction's values
+  if ((tid & 63) == 0) s_scan[tid >> 6] = r;
+  __syncthreads();
+  int32_t total = 0;
+  for (int v = 0; v < NT / 64; ++v) total += s_scan[v];
+  __syncthreads();
+  return total;
+}
+
+// Dequeue tickets of the atomic schedule from a 64-bit word (epoch << 32) |
+// count, where `epoch` is this launch's tag (never 0).  A launch that runs to
+// its end leaves the word at 0; one that does not (an aborted process, a
+// caller that overwrote the memory) may leave any value.  A worker's first
+// ticket therefore claims the word: it reads it and, unless the word already
+// carries this launch's epoch, swaps in (epoch, 1) and holds ticket 0; a
+// worker that loses the swap to another claim takes an ordinary ticket.
+// Every later ticket is one atomic add.  Called by one lane per workgroup.
+__device__ __forceinline__ int32_t first_ticket(unsigned long long* word, uint32_t epoch) {
+  const unsigned long long tagged = ((unsigned long long)epoch << 32) | 1ull;
+  unsigned long long cur = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (;;) {
+    if ((uint32_t)(cur >> 32) == epoch) {
+      const unsigned long long t = atomicAdd(word, 1ull);
+      if ((uint32_t)(t >> 32) == epoch) return (int32_t)(uint32_t)t;
+      cur = t + 1;  // cannot happen while one launch owns the word; claim again
+      continue;
+    }
+    const unsigned long long seen = atomicCAS(word, cur, tagged);
+    if (seen == cur) return 0;
+    cur = seen;
+  }
+}
+__device__ __forceinline__ int32_t next_ticket(unsigned long long* word, uint32_t epoch) {
+  const unsigned long long t = atomicAdd(word, 1ull);
+  if ((uint32_t)(t >> 32) == epoch) return (int32_t)(uint32_t)t;
+  return first_ticket(word, epoch);
 }
 
 // Cooperative zero fill of C[M, cols] (the empty-queue case, :369-371).
@@ -326,8 +397,8 @@ constexpr bool ablk_mode() {
 // epilogue; in atomic mode the ticket of the next tile is taken early in the
 // current one.  `first` is this worker's first item (a ticket in atomic mode).
 template <int BM, int BN, int SBK, int NSTAGE, int NW, class T, int EPI>
-__device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32_t first,
-                                           int n_tiles, const int32_t* s_prefix,
+__device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32_t w_report,
+                                           int32_t first, int n_tiles, const int32_t* s_prefix,
                                            const int32_t* s_offs, int32_t* s_item, uint8_t* lds,
                                            float* s_scale) {
   constexpr int kBK = SBK;                  // K (elements) per stage
@@ -377,6 +448,23 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   const int wn = wave >> 1;
   const int G = gridDim.x;
   const int64_t K = p.k;
+  // Atomic schedule: tickets 0 .. W-1 are drawn in all.  Items past the
+  // first G take one ticket each (W - G of them when W > G) and every worker
+  // with a first item (min(W, G) of them) draws one ticket past the queue
+  // before it stops, so the worker that draws ticket W-1 is the last to touch
+  // the counter: it returns the word to 0 for the next launch and hands the
+  // caller's work_counter the value the reference's counter ends at (W + G,
+  // for the report tile's queue length).  Drawn by lane 0 only.
+  bool claimed = false;
+  auto draw = [&]() -> int32_t {
+    const int32_t t = claimed ? next_ticket(p.counter, p.epoch) : first_ticket(p.counter, p.epoch);
+    claimed = true;
+    if (t == W - 1) {
+      __hip_atomic_store(p.counter, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (p.report != nullptr) atomicExch(p.report, w_report + G);
+    }
+    return G + t;
+  };
   // K < 2^30 (the host bounds (K+8)*ldb_k*2 below 2^31), so stage positions
   // are 32-bit and the full/partial decision stays in scalar registers.
   const int k_size = (int)K;
@@ -856,7 +944,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     __syncthreads();
     // The next tile's ticket, taken after the first wait so that this
     // wave's first DMA wait does not also wait for the atomic.
-    if (take_ticket && tid == 0) ticket = G + atomicAdd(p.counter, 1);
+    if (take_ticket && tid == 0) ticket = draw();
     if constexpr (kABlk) {
       read_kstep_ab(IntConst<0>{}, 0, 0, 0, 0);
       read_kstep_ab(IntConst<0>{}, 0, 0, 0, 1);
@@ -1042,7 +1130,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   // Blocking ticket (used for the first item and to skip a caller queue's
   // invalid items): the leader takes it and broadcasts it through LDS.
   auto take_ticket_now = [&]() -> int32_t {
-    if (tid == 0) *s_item = G + atomicAdd(p.counter, 1);
+    if (tid == 0) *s_item = draw();
     __syncthreads();
     const int32_t t = *s_item;
     __syncthreads();
@@ -1134,14 +1222,24 @@ grouped_gemm_kernel(GemmParams p) {
   __shared__ int32_t s_item;
   __shared__ float s_scale[T::kScaled ? 2 * (BM + BN) : 1];
 
-  const int tid = threadIdx.x;
   const int G = gridDim.x;
   const int n_tiles = (int)((p.n + BN - 1) / BN);
 
-  const int32_t W = p.num_work >= 0
-                        ? p.num_work
-                        : derive_prefix<BM, NT>(p, n_tiles, s_prefix, kOffsLds ? s_offs : nullptr,
-                                                s_scan);
+  // The work_counter's report tile differs from the compute tile when the
+  // caller asked for another tile than the one that runs (the queue length it
+  // reports is the requested tile's, as the reference's counter is).
+  const bool rep_other =
+      p.atomic && p.report != nullptr && (p.report_bm != BM || p.report_bn != BN);
+  const int rep_tiles = rep_other ? (int)((p.n + p.report_bn - 1) / p.report_bn) : 0;
+  int32_t w_report = 0;
+  int32_t W;
+  if (p.num_work >= 0) {
+    W = p.num_work;
+    w_report = rep_other ? queue_length<NT>(p, p.report_bm, rep_tiles, s_scan) : W;
+  } else {
+    W = derive_prefix<BM, NT>(p, n_tiles, s_prefix, kOffsLds ? s_offs : nullptr, s_scan,
+                              rep_tiles, &w_report);
+  }
   if (W == 0) {
     zero_fill(p, EPI == kEpiSwiglu ? p.n / 2 : p.n);
     return;
@@ -1158,29 +1256,13 @@ grouped_gemm_kernel(GemmParams p) {
   // XCD-aware placement), then tickets t of the global counter stand for
   // items G + t; a worker stops at its first ticket past the queue.
   const int32_t first = v;
-  run_worker<BM, BN, SBK, NSTAGE, NW, T, EPI>(p, W, first, n_tiles, s_prefix,
+  run_worker<BM, BN, SBK, NSTAGE, NW, T, EPI>(p, W, w_report, first, n_tiles, s_prefix,
                                          (kOffsLds && p.num_work < 0) ? s_offs : nullptr,
                                          &s_item, lds, s_scale);
-  if (!p.atomic) return;
-  // Every worker has fetched its final (out-of-range) ticket before adding to
-  // `done`, so the last one to arrive reads the final count, returns both
-  // library counters to zero for the next launch on this stream, and hands
-  // the caller's work_counter the value the reference's single counter ends
-  // at, W + G (every item dequeued once, one over-fetch per worker).  Here
-  // items past the first G take one ticket each and every worker that had a
-  // first item over-fetches once, so the counter ends at W and the value
-  // handed over is final + G.
-  if (tid == 0) {
-    if (atomicAdd(p.done, 1) == G - 1) {
-      const int32_t final_count = atomicExch(p.counter, 0);
-      atomicExch(p.done, 0);
-      if (p.report != nullptr) atomicExch(p.report, final_count + G);
-    }
-  }
 }
 
-__global__ void zero_i32_kernel(int32_t* ptr, int count) {
-  for (int i = threadIdx.x; i < count; i += blockDim.x) ptr[i] = 0;
+__global__ void fill_u64_kernel(unsigned long long* ptr, int count, unsigned long long value) {
+  for (int i = threadIdx.x; i < count; i += blockDim.x) ptr[i] = value;
 }
 
 template <class T, int EPI>
@@ -1272,9 +1354,9 @@ int launch_grouped_gemm(int dtype, int epilogue, int block_m, int block_n, const
   return hip_error(hipGetLastError(), "grouped_gemm_kernel launch");
 }
 
-int launch_zero_i32(int32_t* ptr, int count, hipStream_t stream) {
-  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, stream, ptr, count);
-  return hip_error(hipGetLastError(), "zero_i32_kernel launch");
+int launch_fill_u64(unsigned long long* ptr, int count, unsigned long long value, hipStream_t stream) {
+  hipLaunchKernelGGL(fill_u64_kernel, dim3(1), dim3(64), 0, stream, ptr, count, value);
+  return hip_error(hipGetLastError(), "fill_u64_kernel launch");
 }
 
 }  // namespace mgg

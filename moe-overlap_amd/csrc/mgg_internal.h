@@ -39,9 +39,11 @@ struct GemmParams {
   const int32_t* q_expert;  // prebuilt queue (num_work >= 0) or null
   const int32_t* q_tile_m;
   const int32_t* q_tile_n;
-  int32_t* counter;  // atomic mode: library-owned dequeue counter (zero on entry)
-  int32_t* done;     // atomic mode: library-owned exit counter (zero on entry)
-  int32_t* report;   // atomic mode: caller's work_counter, receives the final count, or null
+  // Atomic mode: the library's dequeue counter, a 64-bit word (epoch << 32) |
+  // count.  A word whose epoch is not this launch's is left over from another
+  // launch (any count) and is claimed afresh as count 0.
+  unsigned long long* counter;
+  int32_t* report;   // atomic mode: caller's work_counter, receives W_report + G, or null
   int64_t m;
   int64_t k;
   int64_t n;
@@ -55,6 +57,12 @@ struct GemmParams {
   int32_t num_work;  // < 0: derive the queue from the offsets on the device
   int32_t atomic;
   int32_t remap_xcd;
+  uint32_t epoch;    // atomic mode: this launch's tag in the counter words (never 0)
+  // The tile whose queue length W_report the work_counter reports (W_report
+  // + G): the caller's requested tile, which may differ from the tile the
+  // kernel computes with; the kernel counts it from the offsets.
+  int32_t report_bm;
+  int32_t report_bn;
 };
 
 // Launches the grouped GEMM for one (dtype, epilogue, block_m, block_n) on
@@ -64,8 +72,8 @@ int launch_grouped_gemm(int dtype, int epilogue, int block_m, int block_n, const
 // Whether a fused epilogue is compiled for this tile shape.
 bool epilogue_supported(int epilogue, int block_m, int block_n);
 
-// Zeroes `count` int32 values with a fill kernel on `stream`.
-int launch_zero_i32(int32_t* ptr, int count, hipStream_t stream);
+// Writes `value` to `count` 64-bit words with a fill kernel on `stream`.
+int launch_fill_u64(unsigned long long* ptr, int count, unsigned long long value, hipStream_t stream);
 
 int launch_offsets_from_counts(const void* counts, int counts_type, int64_t num_experts,
                                void* offsets, int out_type, hipStream_t stream);

@@ -24,7 +24,7 @@ from typing import Optional
 import torch
 
 import mgg_native as nat
-from grouped_gemm import persistent_grouped_gemm
+from grouped_gemm import _queue_args, persistent_grouped_gemm
 
 __all__ = [
     "DispatchLayout",
@@ -194,11 +194,13 @@ def expert_mlp_forward(
 
 
 def _grouped_gemm_ex(a, b, offsets, epilogue, out_cols, num_sms, block, use_atomic_queue):
-    """C [M, out_cols] = epilogue(A @ B[e]) over the expert row ranges (queue
-    derived on the device)."""
+    """C [M, out_cols] = epilogue(A @ B[e]) over the expert row ranges, on the
+    block x block kernel tile (queue derived on the device; above 2048
+    experts prebuilt, as the drop-in does)."""
     if epilogue == nat.MGG_EPI_NONE:
         return persistent_grouped_gemm(a, b, offsets, num_sms=num_sms, block_m=block,
-                                       block_n=block, use_atomic_queue=use_atomic_queue)
+                                       block_n=block, use_atomic_queue=use_atomic_queue,
+                                       kernel_tile=(block, block))
     M, K = a.shape
     E, _, N = b.shape
     kmajor = b.stride(1) == 1 and b.stride(2) != 1  # [E, K, N] view of [E, N, K] weights
@@ -207,10 +209,12 @@ def _grouped_gemm_ex(a, b, offsets, epilogue, out_cols, num_sms, block, use_atom
     dtype = _DTYPES[a.dtype] | (nat.MGG_B_KMAJOR if kmajor else 0)
     ldb_rows = b.stride(2) if kmajor else b.stride(1)
     c = torch.empty(M, out_cols, dtype=a.dtype, device=a.device)
+    queue = ("prebuilt" if E > nat.MAX_DEVICE_QUEUE_EXPERTS else "device")
+    we, wm, wn, num_work = _queue_args(queue, offsets, N, block, block)
     with torch.cuda.device(a.device):
         nat.check(nat.lib().mgg_grouped_gemm_ex(
             dtype, epilogue, _p(a), _p(b), _p(c), _p(offsets), M, K, N, E,
-            a.stride(0), b.stride(0), ldb_rows, c.stride(0), block, block,
-            int(num_sms) if num_sms else 0, 1 if use_atomic_queue else 0, None,
-            _stream_ptr(a.device)))
+            a.stride(0), b.stride(0), ldb_rows, c.stride(0), _p(we), _p(wm), _p(wn), num_work,
+            block, block, int(num_sms) if num_sms else 0, 1 if use_atomic_queue else 0, None,
+            0, 0, _stream_ptr(a.device)))
     return c

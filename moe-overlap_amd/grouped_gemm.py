@@ -13,26 +13,35 @@ Differences, all in arguments that do not change results:
 
 * ``num_sms`` defaults to the device's CU count (256 on MI355X) instead of 24;
   an explicit value is honoured (it doubles as a CU-reservation knob).
-* ``block_m``/``block_n`` default to ``None``: 256 x 256 tiles (128 x 256 when
-  the average expert holds fewer than 256 rows).  Explicit values must be 64,
-  128 or 256; they set the tile and queue granularity exactly as before.
+* ``block_m``/``block_n`` (default 128 x 128, as there) are the tile the
+  caller asks for: any power of two >= 16, the tiles the reference's Triton
+  kernel compiles.  They set the queue whose length the atomic schedule's
+  ``work_counter`` reports (W + G, W counted for the requested tile) and the
+  keys of ``_build_work_queue``; the kernel itself computes with the fastest
+  compiled tile, 256 x 256 for bf16/fp16 (eight waves, two per SIMD, 32-deep
+  B stages and 64-deep A blocks), or the tile named by the keyword-only
+  ``kernel_tile``.  Every output element is the same fp32 sum in the same K
+  order whatever the tile, so results do not depend on either choice.
 * ``block_k``, ``num_warps``, ``num_stages`` are accepted and ignored: the
-  kernel's K stage (64), wave count (4) and LDS double buffering are fixed by
-  its design.
+  kernel's K staging, wave count and LDS ring are fixed by its design.
 * ``queue="device"`` (default) derives the same (expert, tile_m, tile_n) queue
   inside the kernel from the offsets, so a call never waits on the device;
   ``queue="prebuilt"`` goes through ``_build_work_queue`` (a host round trip
-  for the cache key, as in the reference).  Outputs are identical.
-* ``work_counter`` (atomic mode) receives the final dequeue count W + G, the
-  value the reference leaves there, while the dequeue itself runs on a
-  library-owned per-stream counter, so no separate zeroing launch is needed.
+  for the cache key, as in the reference).  Outputs are identical.  Above
+  2048 experts (the device-derived queue keeps its tile prefix in LDS) the
+  prebuilt path is taken without being asked.
+* ``work_counter`` (atomic mode) receives the final count W + G, the value
+  the reference leaves there, while the dequeue itself runs on a
+  library-owned per-stream counter word, so no separate zeroing launch is
+  needed.
 * Operands whose inner stride is not 1, whose rows are not 16-byte aligned, or
   with K or N not a multiple of 8, are copied (and zero-padded) on the device
-  first.
+  first.  K == 0 gives zeros, as there.
 """
 from __future__ import annotations
 
 import ctypes
+import operator
 from typing import List, Optional, Tuple, Union
 
 import numpy as np
@@ -49,7 +58,9 @@ __all__ = [
     "quantize_fp8_rows",
 ]
 
-_SUPPORTED_BLOCKS = (64, 128, 256)
+# Tiles compiled into libmgg for bf16/fp16 (fused epilogues: 256x256, 128x128).
+_KERNEL_TILES = ((256, 256), (128, 128), (256, 128), (128, 256), (128, 64), (64, 128),
+                 (64, 64), (256, 64), (64, 256))
 _DTYPE_CODES = {torch.bfloat16: _nat.MGG_DTYPE_BF16, torch.float16: _nat.MGG_DTYPE_FP16}
 
 _WORK_QUEUE_CACHE: dict = {}
@@ -140,7 +151,8 @@ def _build_work_queue(
     Reference: src/triton_grouped_gemm.py:240-297.  Cached by (offsets bytes,
     n_size, block_m, block_n) with FIFO eviction at 32 entries; the offsets
     are copied to the host for the key (a device sync, as in the reference).
-    Built by libmgg on the offsets' device.
+    Built by libmgg on the offsets' device (on the host, then copied, above
+    the device builder's 8192 experts).
     """
     assert expert_offsets.dim() == 1
     if block_m <= 0 or block_n <= 0:
@@ -159,7 +171,17 @@ def _build_work_queue(
     wn = torch.empty(total, dtype=torch.int32, device=device)
     lib = _nat.lib()
     if total > 0:
-        if device.type == "cuda":
+        if device.type == "cuda" and num_experts > _nat.MAX_DEVICE_BUILDER_EXPERTS:
+            host_q = [torch.empty(total, dtype=torch.int32) for _ in range(3)]
+            _nat.check(
+                lib.mgg_build_work_queue_host(
+                    host.ctypes.data_as(ctypes.c_void_p), num_experts, int(n_size),
+                    int(block_m), int(block_n), *(_ptr(q) for q in host_q), total,
+                )
+            )
+            for dst, src in zip((we, wm, wn), host_q):
+                dst.copy_(src)
+        elif device.type == "cuda":
             off32 = expert_offsets.to(torch.int32).contiguous()
             with torch.cuda.device(device):
                 _nat.check(
@@ -185,7 +207,7 @@ def _build_work_queue(
 # --------------------------------------------------------------------------
 # grouped GEMM
 # --------------------------------------------------------------------------
-def _default_blocks(m_total: int, num_experts: int) -> Tuple[int, int]:
+def _default_kernel_tile(m_total: int, num_experts: int) -> Tuple[int, int]:
     """256x256 for every expert size.  Rows of a tile past its expert's end are
     zero-fill DMAs that read nothing, so a tile's cost follows the memory
     requests of its valid rows, and the 256x256 kernel (two waves per SIMD)
@@ -196,6 +218,22 @@ def _default_blocks(m_total: int, num_experts: int) -> Tuple[int, int]:
     256-384 rows 101-119 against 140-192."""
     del m_total, num_experts
     return 256, 256
+
+
+def _requested_tile(block_m, block_n) -> Tuple[int, int]:
+    """The caller's block_m x block_n: powers of two >= 16, the tile edges the
+    reference's Triton kernel compiles (tl.arange needs a power of two, tl.dot
+    at least 16; src/triton_grouped_gemm.py:54-56, :67-69)."""
+    out = []
+    for name, v in (("block_m", block_m), ("block_n", block_n)):
+        try:
+            v = operator.index(v)
+        except TypeError:
+            raise ValueError(f"{name} must be an int.") from None
+        if v < 16 or v & (v - 1) or v > 1 << 20:
+            raise ValueError(f"{name} must be a power of two >= 16 (got {v}).")
+        out.append(v)
+    return out[0], out[1]
 
 
 def _fast_layout(t: torch.Tensor) -> bool:
@@ -232,8 +270,8 @@ def persistent_grouped_gemm(
     b_expert: torch.Tensor,
     expert_offsets: torch.Tensor,
     num_sms: Optional[int] = None,
-    block_m: Optional[int] = None,
-    block_n: Optional[int] = None,
+    block_m: int = 128,
+    block_n: int = 128,
     block_k: int = 32,
     use_atomic_queue: bool = True,
     work_counter: Optional[torch.Tensor] = None,
@@ -241,6 +279,7 @@ def persistent_grouped_gemm(
     num_stages: int = 3,
     *,
     queue: str = "device",
+    kernel_tile: Optional[Tuple[int, int]] = None,
     a_scale: Optional[torch.Tensor] = None,
     b_scale: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
@@ -255,6 +294,10 @@ def persistent_grouped_gemm(
     layer's weight, which the reference's Triton kernel reads through its
     strides): it is read in place, with results bitwise equal to those of the
     same values stored [E, K, N]; other layouts are copied first.
+
+    block_m x block_n is the requested tile (queue granularity and the
+    work_counter's W + G); kernel_tile, when given, names the compiled tile
+    the kernel computes with (default: the fastest, see _default_kernel_tile).
 
     Extension beyond the reference (which rejects fp8, :357-358): with
     float8_e4m3fn a_cat and b_expert plus a_scale [M] (per token) and b_scale
@@ -273,41 +316,34 @@ def persistent_grouped_gemm(
         raise ValueError("expert_offsets must have shape [num_experts + 1].")
     if expert_offsets.device != a_cat.device:
         raise ValueError("expert_offsets must be on the same device as input tensors.")
+    if queue not in ("device", "prebuilt"):
+        raise ValueError("queue must be 'device' or 'prebuilt'.")
+    rep_m, rep_n = _requested_tile(block_m, block_n)
     if a_cat.dtype == torch.float8_e4m3fn:
         return _persistent_grouped_gemm_fp8(a_cat, b_expert, expert_offsets, a_scale, b_scale,
-                                            num_sms, block_m, block_n, use_atomic_queue,
-                                            work_counter)
+                                            num_sms, rep_m, rep_n, kernel_tile, use_atomic_queue,
+                                            work_counter, queue)
     if a_cat.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("a_cat dtype must be bf16/fp16.")
     if b_expert.dtype != a_cat.dtype:
         raise ValueError("b_expert dtype should match a_cat dtype.")
-    if queue not in ("device", "prebuilt"):
-        raise ValueError("queue must be 'device' or 'prebuilt'.")
     if queue == "device" and b_expert.size(0) > _nat.MAX_DEVICE_QUEUE_EXPERTS:
         queue = "prebuilt"  # the device-derived queue keeps its tile prefix in LDS
 
     m_total, k_size = a_cat.shape
     num_experts, _, n_size = b_expert.shape
-    if block_m is None or block_n is None:
-        dm, dn = _default_blocks(m_total, num_experts)
-        block_m = dm if block_m is None else block_m
-        block_n = dn if block_n is None else block_n
-    if block_m not in _SUPPORTED_BLOCKS or block_n not in _SUPPORTED_BLOCKS:
-        raise ValueError("block_m and block_n must each be one of 64, 128, 256.")
+    if kernel_tile is None:
+        kernel_tile = _default_kernel_tile(m_total, num_experts)
+    kbm, kbn = (int(v) for v in kernel_tile)
+    if (kbm, kbn) not in _KERNEL_TILES:
+        raise ValueError(f"kernel_tile must be one of {_KERNEL_TILES}.")
     device = a_cat.device
     dev_index = device.index if device.index is not None else torch.cuda.current_device()
     if num_sms is None:
         num_sms = _cu_count(dev_index)
     if int(num_sms) <= 0:
         raise ValueError("num_sms must be positive.")
-
-    counter_dev = None
-    if use_atomic_queue and work_counter is not None:
-        if work_counter.numel() != 1 or work_counter.dtype != torch.int32:
-            raise ValueError("work_counter must be int32 tensor of shape [1].")
-        counter_dev = work_counter.to(device)
-        if not counter_dev.is_contiguous():
-            counter_dev = counter_dev.contiguous()
+    counter_dev = _counter_arg(work_counter, use_atomic_queue, device)
 
     # K or N not a multiple of 8: zero-pad on the device (zeros add nothing).
     k_pad = (k_size + 7) // 8 * 8
@@ -320,11 +356,13 @@ def persistent_grouped_gemm(
         b_op = torch.nn.functional.pad(b_op, (0, 0, 0, k_pad - k_size))
     if n_pad != n_size:
         b_op = torch.nn.functional.pad(b_op, (0, n_pad - n_size))
-    a_op = _gemm_operand(a_op)
-    if not b_kmajor:
-        b_op = _gemm_operand(b_op)
-    # Leading dimensions; a size-1 dimension's stride is never used.  ldb_k is
-    # the stride between B's rows: K rows, or N rows for K-major B.
+    if k_pad > 0:
+        a_op = _gemm_operand(a_op)
+        if not b_kmajor:
+            b_op = _gemm_operand(b_op)
+    # Leading dimensions; a size-1 dimension's stride is never used, nor are
+    # A's and B's when K == 0.  ldb_k is the stride between B's rows: K rows,
+    # or N rows for K-major B.
     lda = a_op.stride(0) if m_total > 1 else k_pad
     if b_kmajor:
         ldb_k = b_op.stride(2)
@@ -335,39 +373,63 @@ def persistent_grouped_gemm(
     dtype_code = _DTYPE_CODES[a_cat.dtype] | (_nat.MGG_B_KMAJOR if b_kmajor else 0)
     c_op = torch.empty((m_total, n_pad), device=device, dtype=a_cat.dtype)
 
-    if queue == "prebuilt":
-        we, wm, wn = _build_work_queue(expert_offsets, n_size=n_size, block_m=block_m, block_n=block_n)
-        num_work = we.numel()
-    else:
-        we = wm = wn = None
-        num_work = -1
-    off32 = expert_offsets if expert_offsets.dtype == torch.int32 else expert_offsets.to(torch.int32)
-    off32 = off32.contiguous()
-
+    we, wm, wn, num_work = _queue_args(queue, expert_offsets, n_size, kbm, kbn)
+    off32 = _offsets_i32(expert_offsets)
     args = (
         dtype_code, _ptr(a_op), _ptr(b_op), _ptr(c_op),
         _ptr(off32), m_total, k_pad, n_pad,
         num_experts, lda, ldb_e, ldb_k, c_op.stride(0),
         _ptr(we), _ptr(wm), _ptr(wn), num_work,
-        int(block_m), int(block_n), int(num_sms), 1 if use_atomic_queue else 0,
-        _ptr(counter_dev), torch.cuda.current_stream(device).cuda_stream,
+        kbm, kbn, int(num_sms), 1 if use_atomic_queue else 0,
+        _ptr(counter_dev), rep_m, rep_n, torch.cuda.current_stream(device).cuda_stream,
     )
-    lib = _nat.lib()
-    # The library launches on the calling thread's current HIP device.
-    if torch.cuda.current_device() == dev_index:
-        _nat.check(lib.mgg_grouped_gemm(*args))
-    else:
-        with torch.cuda.device(dev_index):
-            _nat.check(lib.mgg_grouped_gemm(*args))
+    _launch(_nat.lib().mgg_grouped_gemm, args, dev_index)
     if n_pad != n_size:
         return c_op[:, :n_size].contiguous()
     return c_op
 
 
-_FP8_BLOCK_M = (256, 192, 128)
+def _counter_arg(work_counter, use_atomic_queue, device):
+    """The device int32 [1] that receives W + G in atomic mode, or None.  As in
+    the reference (:377-384), a counter on another device is copied there and
+    the copy receives the count."""
+    if not use_atomic_queue or work_counter is None:
+        return None
+    if work_counter.numel() != 1 or work_counter.dtype != torch.int32:
+        raise ValueError("work_counter must be int32 tensor of shape [1].")
+    counter_dev = work_counter.to(device)
+    return counter_dev if counter_dev.is_contiguous() else counter_dev.contiguous()
 
 
-def _default_fp8_blocks(m_total: int, num_experts: int) -> Tuple[int, int]:
+def _offsets_i32(expert_offsets: torch.Tensor) -> torch.Tensor:
+    off32 = expert_offsets if expert_offsets.dtype == torch.int32 else expert_offsets.to(torch.int32)
+    return off32.contiguous()
+
+
+def _queue_args(queue, expert_offsets, n_size, kbm, kbn):
+    """(work_expert, work_tile_m, work_tile_n, num_work) for the kernel tile:
+    the prebuilt queue of _build_work_queue, or no arrays and -1 (derived on
+    the device)."""
+    if queue == "prebuilt":
+        we, wm, wn = _build_work_queue(expert_offsets, n_size=n_size, block_m=kbm, block_n=kbn)
+        return we, wm, wn, we.numel()
+    return None, None, None, -1
+
+
+def _launch(fn, args, dev_index: int) -> None:
+    """Calls a libmgg launch entry point with dev_index as the current HIP
+    device (the library launches on the calling thread's current device)."""
+    if torch.cuda.current_device() == dev_index:
+        _nat.check(fn(*args))
+    else:
+        with torch.cuda.device(dev_index):
+            _nat.check(fn(*args))
+
+
+_FP8_KERNEL_TILES = ((256, 256), (256, 128), (192, 128), (128, 128))
+
+
+def _default_fp8_kernel_tile(m_total: int, num_experts: int) -> Tuple[int, int]:
     """fp8 tile by the average rows per expert (top-k routing spreads the
     counts around it): 128x128 up to 128 rows, 256x128 for 129-256 (one tile
     holds most experts), 256x256 above.  Measured on MI355X at E=64, K=2048,
@@ -388,7 +450,8 @@ def _default_fp8_blocks(m_total: int, num_experts: int) -> Tuple[int, int]:
 
 
 def _persistent_grouped_gemm_fp8(a_cat, b_expert, expert_offsets, a_scale, b_scale, num_sms,
-                                 block_m, block_n, use_atomic_queue, work_counter):
+                                 rep_m, rep_n, kernel_tile, use_atomic_queue, work_counter,
+                                 queue):
     if b_expert.dtype != torch.float8_e4m3fn:
         raise ValueError("b_expert dtype should match a_cat dtype.")
     if a_scale is None or b_scale is None:
@@ -401,54 +464,50 @@ def _persistent_grouped_gemm_fp8(a_cat, b_expert, expert_offsets, a_scale, b_sca
         raise ValueError("scales must be on the same device as input tensors.")
     device = a_cat.device
     dev_index = device.index if device.index is not None else torch.cuda.current_device()
-    if block_m is None or block_n is None:
-        dm, dn = _default_fp8_blocks(m_total, num_experts)
-        block_m = block_m or dm
-        block_n = block_n or dn
-    if not ((block_n == 128 and block_m in _FP8_BLOCK_M) or (block_m, block_n) == (256, 256)):
-        raise ValueError("fp8 tiles are block_m x block_n = 256x256, 256x128, 192x128 or 128x128.")
+    if kernel_tile is None:
+        kernel_tile = _default_fp8_kernel_tile(m_total, num_experts)
+    kbm, kbn = (int(v) for v in kernel_tile)
+    if (kbm, kbn) not in _FP8_KERNEL_TILES:
+        raise ValueError(f"fp8 kernel_tile must be one of {_FP8_KERNEL_TILES}.")
+    if queue == "device" and num_experts > _nat.MAX_DEVICE_QUEUE_EXPERTS:
+        queue = "prebuilt"
     if num_sms is None:
         num_sms = _cu_count(dev_index)
-    counter_dev = None
-    if use_atomic_queue and work_counter is not None:
-        if work_counter.numel() != 1 or work_counter.dtype != torch.int32:
-            raise ValueError("work_counter must be int32 tensor of shape [1].")
-        counter_dev = work_counter.to(device).contiguous()
+    if int(num_sms) <= 0:
+        raise ValueError("num_sms must be positive.")
+    counter_dev = _counter_arg(work_counter, use_atomic_queue, device)
     # K to a multiple of 16, N to a multiple of 8 (zero padding adds nothing).
     k_pad = (k_size + 15) // 16 * 16
     n_pad = (n_size + 7) // 8 * 8
     a_op = a_cat
     if k_pad != k_size:
         a_op = torch.nn.functional.pad(a_op.view(torch.uint8), (0, k_pad - k_size)).view(a_cat.dtype)
-    if a_op.stride(1) != 1 or a_op.stride(0) % 16 or a_op.data_ptr() % 16:
+    if k_pad > 0 and (a_op.stride(1) != 1 or a_op.stride(0) % 16 or a_op.data_ptr() % 16):
         a_op = a_op.contiguous()
     b_nk = b_expert.transpose(1, 2)  # [E, N, K]
     if k_pad != k_size or n_pad != n_size:
         b_nk = torch.nn.functional.pad(b_nk.contiguous().view(torch.uint8),
                                        (0, k_pad - k_size, 0, n_pad - n_size)).view(b_expert.dtype)
-    if b_nk.stride(2) != 1 or b_nk.stride(1) % 16 or b_nk.stride(0) % 16 or b_nk.data_ptr() % 16:
+    if k_pad > 0 and (b_nk.stride(2) != 1 or b_nk.stride(1) % 16 or b_nk.stride(0) % 16
+                      or b_nk.data_ptr() % 16):
         b_nk = b_nk.contiguous()
     sa = a_scale.reshape(-1).to(torch.float32).contiguous()
     sb = b_scale.reshape(num_experts, n_size).to(torch.float32)
     if n_pad != n_size:
         sb = torch.nn.functional.pad(sb, (0, n_pad - n_size))
     sb = sb.contiguous()
-    off32 = expert_offsets if expert_offsets.dtype == torch.int32 else expert_offsets.to(torch.int32)
-    off32 = off32.contiguous()
+    off32 = _offsets_i32(expert_offsets)
     c_op = torch.empty((m_total, n_pad), device=device, dtype=torch.bfloat16)
     lda = a_op.stride(0) if m_total > 1 else k_pad
     ldb_n = b_nk.stride(1) if n_pad > 1 else k_pad
     ldb_e = b_nk.stride(0) if num_experts > 1 else n_pad * ldb_n
+    we, wm, wn, num_work = _queue_args(queue, expert_offsets, n_size, kbm, kbn)
     args = (_ptr(a_op), _ptr(b_nk), _ptr(c_op), _ptr(off32), _ptr(sa), _ptr(sb),
             m_total, k_pad, n_pad, num_experts, lda, ldb_e, ldb_n, c_op.stride(0),
-            int(block_m), int(block_n), int(num_sms), 1 if use_atomic_queue else 0,
-            _ptr(counter_dev), torch.cuda.current_stream(device).cuda_stream)
-    lib = _nat.lib()
-    if torch.cuda.current_device() == dev_index:
-        _nat.check(lib.mgg_grouped_gemm_fp8(*args))
-    else:
-        with torch.cuda.device(dev_index):
-            _nat.check(lib.mgg_grouped_gemm_fp8(*args))
+            _ptr(we), _ptr(wm), _ptr(wn), num_work,
+            kbm, kbn, int(num_sms), 1 if use_atomic_queue else 0,
+            _ptr(counter_dev), rep_m, rep_n, torch.cuda.current_stream(device).cuda_stream)
+    _launch(_nat.lib().mgg_grouped_gemm_fp8, args, dev_index)
     if n_pad != n_size:
         return c_op[:, :n_size].contiguous()
     return c_op

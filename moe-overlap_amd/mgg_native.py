@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime this library must share)
 
 LIB_PATH = Path(__file__).resolve().parent / "libmgg.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 MGG_OK = 0
 MGG_ERR_INVALID = 1
@@ -29,6 +29,9 @@ MGG_INT64 = 1
 # Largest expert count for which the kernels derive the work queue on the
 # device (the per-expert tile prefix lives in LDS; kMaxLdsExpertsGemm).
 MAX_DEVICE_QUEUE_EXPERTS = 2048
+# Largest expert count of the device-side queue builder mgg_build_work_queue
+# (kMaxLdsExpertsQueue).
+MAX_DEVICE_BUILDER_EXPERTS = 8192
 
 MGG_EPI_NONE = 0
 MGG_EPI_GELU = 1
@@ -56,22 +59,25 @@ _SIGNATURES = {
         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,  # E, lda, ldb_e, ldb_k, ldc
         _c_ptr, _c_ptr, _c_ptr, _c_i64,  # queue, num_work
         _c_i32, _c_i32, _c_i32, _c_i32,  # block_m, block_n, num_workers, atomic
-        _c_ptr, _c_ptr,  # work_counter, stream
+        _c_ptr, _c_i32, _c_i32, _c_ptr,  # work_counter, report_block_m/n, stream
     ],
     "mgg_grouped_gemm_ex": [
         _c_i32, _c_i32, _c_ptr, _c_ptr, _c_ptr,  # dtype, epilogue, a, b, c
         _c_ptr, _c_i64, _c_i64, _c_i64,  # offsets, M, K, N
         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,  # E, lda, ldb_e, ldb_k, ldc
+        _c_ptr, _c_ptr, _c_ptr, _c_i64,  # queue, num_work
         _c_i32, _c_i32, _c_i32, _c_i32,  # block_m, block_n, num_workers, atomic
-        _c_ptr, _c_ptr,  # work_counter, stream
+        _c_ptr, _c_i32, _c_i32, _c_ptr,  # work_counter, report_block_m/n, stream
     ],
     "mgg_grouped_gemm_fp8": [
         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,  # a, b, c, offsets, a_scale, b_scale
         _c_i64, _c_i64, _c_i64, _c_i64,  # M, K, N, E
         _c_i64, _c_i64, _c_i64, _c_i64,  # lda, ldb_e, ldb_n, ldc
+        _c_ptr, _c_ptr, _c_ptr, _c_i64,  # queue, num_work
         _c_i32, _c_i32, _c_i32, _c_i32,  # block_m, block_n, num_workers, atomic
-        _c_ptr, _c_ptr,  # work_counter, stream
+        _c_ptr, _c_i32, _c_i32, _c_ptr,  # work_counter, report_block_m/n, stream
     ],
+    "mgg_debug_set_dequeue_counter": [ctypes.c_uint64, _c_ptr],
     "mgg_dispatch_layout": [
         _c_ptr, _c_i32, _c_i64, _c_i32, _c_i64,  # topk_idx, idx_type, T, top_k, E
         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,  # counts, offsets, slot_pos, token_index, row_assign

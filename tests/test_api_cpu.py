@@ -80,5 +80,32 @@ def test_flops_helper():
 def test_default_fp8_tile(avg, want):
     """128x128 up to 128 rows per expert, 256x128 for 129-256, else 256x256;
     the fp8 benchmark config (64 experts, 24576 rows: 384 per expert) takes 256x256."""
-    assert gg._default_fp8_blocks(avg * 64, 64) == want
-    assert gg._default_fp8_blocks(0, 0) == (128, 128)
+    assert gg._default_fp8_kernel_tile(avg * 64, 64) == want
+    assert gg._default_fp8_kernel_tile(0, 0) == (128, 128)
+
+
+@pytest.mark.parametrize("edge", [16, 32, 64, 128, 256, 512, 1024, 1 << 20])
+def test_requested_tile_accepts_triton_tiles(edge):
+    """Every power of two >= 16 (what tl.arange and tl.dot accept,
+    src/triton_grouped_gemm.py:54-56, :67-69) is a valid requested tile."""
+    assert gg._requested_tile(edge, 16) == (edge, 16)
+    assert gg._requested_tile(np.int64(edge), edge) == (edge, edge)
+
+
+@pytest.mark.parametrize("bad", [0, -128, 1, 8, 24, 48, 96, 100, 2 ** 21, 128.0, "128", None])
+def test_requested_tile_rejects_others(bad):
+    with pytest.raises(ValueError):
+        gg._requested_tile(bad, 128)
+    with pytest.raises(ValueError):
+        gg._requested_tile(128, bad)
+
+
+def test_large_expert_queue_builds_on_host():
+    """Above the device builder's 8192 experts the queue is built by the host
+    builder (CPU offsets here take that path always); checked against the oracle."""
+    rng = np.random.default_rng(3)
+    counts = rng.integers(0, 300, 9000)
+    offs = torch.from_numpy(np.concatenate([[0], np.cumsum(counts)]).astype(np.int64))
+    got = gg._build_work_queue(offs, 300, 128, 256)
+    for g, w in zip(got, orc.build_work_queue(offs.numpy(), 300, 128, 256)):
+        np.testing.assert_array_equal(g.numpy(), w)

@@ -62,7 +62,7 @@ def test_fp8_small_ragged(cuda_device, block_m, block_n, atomic):
     log(f"fp8 small {block_m}x{block_n} atomic={atomic}")
     counts = [37, 0, 300, 5, 129]
     a, sa, b, sb, offs = fp8_inputs(counts, 512, 320, device=cuda_device)
-    c = gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, block_m=block_m, block_n=block_n,
+    c = gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, kernel_tile=(block_m, block_n),
                                    use_atomic_queue=atomic, a_scale=sa, b_scale=sb)
     assert c.dtype == torch.bfloat16 and tuple(c.shape) == (a.shape[0], 320)
     assert_close_fp8(c, a, sa, b, sb, offs)
@@ -83,7 +83,7 @@ def test_fp8_random_shapes(cuda_device, seed):
     bm, bn = ((256, 128), (192, 128), (128, 128), (256, 256))[seed % 4]
     log(f"fp8 random seed={seed} counts={counts.tolist()} K={k} N={n} block={bm}x{bn}")
     a, sa, b, sb, offs = fp8_inputs(counts.tolist(), k, n, seed=seed, device=cuda_device)
-    outs = [gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, block_m=bm, block_n=bn,
+    outs = [gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, kernel_tile=(bm, bn),
                                        use_atomic_queue=atomic, a_scale=sa, b_scale=sb,
                                        num_sms=int(rng.integers(1, 300)))
             for atomic in (False, True)]
@@ -112,8 +112,8 @@ def test_fp8_work_counter_and_errors(cuda_device):
     assert int(wc.item()) == 2 * 3 * 2 + 7  # W = sum ceil(300/128) * ceil(256/128)
     with pytest.raises(ValueError, match="a_scale"):
         gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs)
-    with pytest.raises(ValueError, match="256x256, 256x128, 192x128 or 128x128"):
-        gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, block_m=64, block_n=64,
+    with pytest.raises(ValueError, match="fp8 kernel_tile"):
+        gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, kernel_tile=(64, 64),
                                    a_scale=sa, b_scale=sb)
 
 
@@ -126,12 +126,12 @@ def test_fp8_baseline_config(cuda_device):
     log("fp8 cfg5")
     case = workloads.make_fp8_case(device=cuda_device, keep_reference=True)
     offs = gg.expert_offsets_from_recv_counts(case.counts, device=cuda_device)
-    assert gg._default_fp8_blocks(case.m, case.num_experts) == (256, 256)
+    assert gg._default_fp8_kernel_tile(case.m, case.num_experts) == (256, 256)
     c = gg.persistent_grouped_gemm(case.a, case.b_nk.transpose(1, 2), offs,
                                    a_scale=case.a_scale, b_scale=case.b_scale)
     for bm, bn in ((256, 128), (128, 128), (192, 128)):
-        other = gg.persistent_grouped_gemm(case.a, case.b_nk.transpose(1, 2), offs, block_m=bm,
-                                           block_n=bn, a_scale=case.a_scale, b_scale=case.b_scale)
+        other = gg.persistent_grouped_gemm(case.a, case.b_nk.transpose(1, 2), offs, kernel_tile=(bm, bn),
+                                           a_scale=case.a_scale, b_scale=case.b_scale)
         assert torch.equal(c, other), (bm, bn)
     c = c.float()
     o = offs.cpu().tolist()

@@ -89,7 +89,7 @@ def test_small_ragged_parity_all_modes(cuda_device, case, dtype):
         for atomic in (False, True):
             for queue in ("device", "prebuilt"):
                 log(f"case={case} dtype={dtype} blocks={blocks} atomic={atomic} queue={queue}")
-                c = gg.persistent_grouped_gemm(a, b, offs, block_m=blocks[0], block_n=blocks[1],
+                c = gg.persistent_grouped_gemm(a, b, offs, kernel_tile=blocks,
                                                use_atomic_queue=atomic, queue=queue)
                 torch.cuda.synchronize()
                 assert_parity(c, a, b, offs, k)
@@ -120,7 +120,7 @@ def test_k_staging_edges_256x256(cuda_device, k, dtype):
     outs = []
     for atomic in (False, True):
         log(f"k={k} dtype={dtype} atomic={atomic}")
-        c = gg.persistent_grouped_gemm(a, b, offs, block_m=256, block_n=256, use_atomic_queue=atomic)
+        c = gg.persistent_grouped_gemm(a, b, offs, kernel_tile=(256, 256), use_atomic_queue=atomic)
         torch.cuda.synchronize()
         assert_parity(c, a, b, offs, k)
         outs.append(c)
@@ -153,7 +153,7 @@ def test_random_shapes_match_oracle(cuda_device, seed):
     outs = []
     for atomic in (False, True):
         for queue in ("device", "prebuilt"):
-            c = gg.persistent_grouped_gemm(a, b, offs, block_m=blocks[0], block_n=blocks[1],
+            c = gg.persistent_grouped_gemm(a, b, offs, kernel_tile=blocks,
                                            use_atomic_queue=atomic, queue=queue,
                                            num_sms=int(7 + 37 * seed) % 300 + 1)
             torch.cuda.synchronize()
@@ -169,7 +169,7 @@ def test_cpu_plumbing_config_in_bf16(cuda_device):
     offs = gg.expert_offsets_from_recv_counts(case.counts, device=cuda_device)
     a, b = case.a.to(cuda_device), case.b.to(cuda_device)
     for atomic in (False, True):
-        c = gg.persistent_grouped_gemm(a, b, offs, block_m=128, block_n=128, use_atomic_queue=atomic)
+        c = gg.persistent_grouped_gemm(a, b, offs, kernel_tile=(128, 128), use_atomic_queue=atomic)
         assert_parity(c, a, b, offs, case.k)
 
 
@@ -201,8 +201,8 @@ def test_full_size_configs(cuda_device, name):
     for blocks in [(256, 256), (128, 128)]:
         for atomic in (False, True):
             log(f"  blocks={blocks} atomic={atomic}")
-            c = gg.persistent_grouped_gemm(case_gpu_a, case_gpu_b, offs, block_m=blocks[0],
-                                           block_n=blocks[1], use_atomic_queue=atomic)
+            c = gg.persistent_grouped_gemm(case_gpu_a, case_gpu_b, offs, kernel_tile=blocks,
+                                           use_atomic_queue=atomic)
             torch.cuda.synchronize()
             sampled_parity(c, case, offs)
             outs.append(c)
@@ -261,7 +261,7 @@ def test_many_experts(cuda_device, num_experts):
     for blocks in [(64, 64), (256, 256)]:
         for atomic in (False, True):
             log(f"E={num_experts} blocks={blocks} atomic={atomic}")
-            c = gg.persistent_grouped_gemm(a, b, offs, block_m=blocks[0], block_n=blocks[1],
+            c = gg.persistent_grouped_gemm(a, b, offs, kernel_tile=blocks,
                                            use_atomic_queue=atomic)
             torch.cuda.synchronize()
             assert_parity(c, a, b, offs, 64)
@@ -297,7 +297,7 @@ def test_rows_outside_experts_are_not_written(cuda_device):
         nat.check(nat.lib().mgg_grouped_gemm(
             nat.MGG_DTYPE_BF16, a_full.data_ptr(), b.data_ptr(), c.data_ptr(), offs_shift.data_ptr(),
             m, 64, 128, 3, 64, 64 * 128, 128, 128, None, None, None, -1, 64, 64, 5, atomic, None,
-            torch.cuda.current_stream().cuda_stream))
+            0, 0, torch.cuda.current_stream().cuda_stream))
         torch.cuda.synchronize()
         assert bool((c[:2] == 123).all()) and bool((c[16:] == 123).all())
         want = oracle_out(a, b, offs)
@@ -329,7 +329,7 @@ def test_caller_queue_with_invalid_items(cuda_device):
             nat.MGG_DTYPE_BF16, a.data_ptr(), b.data_ptr(), c.data_ptr(), offs.data_ptr(),
             m, k, n, len(counts), k, k * n, n, n, qe.data_ptr(), qm.data_ptr(), qn.data_ptr(),
             len(q), bm, bn, 7, atomic, counter.data_ptr() if atomic else None,
-            torch.cuda.current_stream().cuda_stream))
+            0, 0, torch.cuda.current_stream().cuda_stream))
         torch.cuda.synchronize()
         assert_parity(c, a, b, offs, k)
         if atomic:
@@ -403,9 +403,9 @@ def test_kmajor_b_is_read_in_place_bitwise(cuda_device, case, dtype):
     for blocks in ALL_BLOCKS:
         for atomic in (False, True):
             log(f"kmajor case={case} dtype={dtype} blocks={blocks} atomic={atomic}")
-            c_n = gg.persistent_grouped_gemm(a, b, offs, block_m=blocks[0], block_n=blocks[1],
+            c_n = gg.persistent_grouped_gemm(a, b, offs, kernel_tile=blocks,
                                              use_atomic_queue=atomic)
-            c_k = gg.persistent_grouped_gemm(a, b_km, offs, block_m=blocks[0], block_n=blocks[1],
+            c_k = gg.persistent_grouped_gemm(a, b_km, offs, kernel_tile=blocks,
                                              use_atomic_queue=atomic)
             torch.cuda.synchronize()
             assert torch.equal(c_k[: mask.numel()][mask], c_n[: mask.numel()][mask]), (blocks, atomic)

@@ -91,7 +91,7 @@ FAKE = 1 << 20  # a 16-byte aligned non-null address; validation rejects before 
 def gemm_call(**over):
     args = dict(dtype=nat.MGG_DTYPE_BF16, a=FAKE, b=FAKE, c=FAKE, off=FAKE, m=64, k=64, n=64, e=1,
                 lda=64, ldb_e=64 * 64, ldb_k=64, ldc=64, we=None, wm=None, wn=None, nw=-1,
-                bm=128, bn=128, workers=4, atomic=0, counter=None, stream=None)
+                bm=128, bn=128, workers=4, atomic=0, counter=None, rbm=0, rbn=0, stream=None)
     args.update(over)
     return nat.lib().mgg_grouped_gemm(*args.values())
 

@@ -114,12 +114,20 @@ def test_interleave_gate_up_columns():
             np.testing.assert_array_equal(w[:, :, 64 * q + 32 + c], u[:, :, 32 * q + c])
 
 
-def test_gelu_and_silu_closed_forms():
-    x = np.array([-3.0, -1.0, 0.0, 0.5, 2.0])
-    ref = torch.nn.functional.gelu(torch.tensor(x, dtype=torch.float64)).numpy()
-    np.testing.assert_allclose(mo.gelu(x), ref, rtol=1e-12, atol=1e-12)
-    np.testing.assert_allclose(mo.silu(x), x / (1 + np.exp(-x)), rtol=1e-15)
-    assert mo.gelu(np.array([0.0]))[0] == 0.0
+def test_gelu_and_silu_match_torch():
+    """The oracle's activations against torch's own (train:86-93 uses
+    nn.GELU; SwiGLU's gate is F.silu) in float64, over [-100, 100] and out to
+    where e^-x overflows (x < -709: silu's limit there is -0.0), plus the
+    values the definitions fix: gelu(0) = silu(0) = 0, silu(x) -> x."""
+    x = np.concatenate([np.linspace(-100.0, 100.0, 20001), [-800.0, -710.0, -709.0, 709.0, 800.0]])
+    xt = torch.tensor(x, dtype=torch.float64)
+    np.testing.assert_allclose(mo.gelu(x), torch.nn.functional.gelu(xt).numpy(),
+                               rtol=1e-12, atol=1e-300)
+    with np.errstate(over="ignore"):
+        got = mo.silu(x)
+    np.testing.assert_allclose(got, torch.nn.functional.silu(xt).numpy(), rtol=1e-13, atol=1e-300)
+    assert mo.gelu(np.array([0.0]))[0] == 0.0 and mo.silu(np.array([0.0]))[0] == 0.0
+    assert got[-1] == 800.0 and got[np.argmin(x)] == 0.0
 
 
 def per_token_mlp(x, idx, w, w1, w2, activation):
@@ -137,7 +145,7 @@ def per_token_mlp(x, idx, w, w1, w2, activation):
                 F = h.size // 2
                 gate = np.concatenate([h[64 * q: 64 * q + 32] for q in range(F // 32)])
                 up = np.concatenate([h[64 * q + 32: 64 * q + 64] for q in range(F // 32)])
-                h = gate / (1 + np.exp(-gate)) * up
+                h = torch.nn.functional.silu(torch.from_numpy(gate)).numpy() * up
             out[t] += w[t, j] * (h @ w2[e].astype(np.float64))
     return out
 
