@@ -245,6 +245,22 @@ int mgg_dispatch_layout(const void* topk_idx, int idx_type, int64_t num_tokens, 
                         void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * mgg_dispatch_layout without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * workspace is a 1 MiB array inside the library (one per device, held until
+ * the process ends): layouts whose mgg_dispatch_layout_workspace_bytes()
+ * exceeds 1 MiB (e.g. more than 262144 assignments over 1024 experts) are
+ * rejected with MGG_ERR_UNSUPPORTED.  No memory is allocated.  Every call
+ * on one device shares that array: calls that overlap on one device (on
+ * unordered streams) race.  Results are those of mgg_dispatch_layout.
+ */
+int mgg_dispatch_layout_noalloc(const void* topk_idx, int idx_type, int64_t num_tokens, int top_k,
+                                int64_t num_experts, int32_t* counts, int32_t* offsets,
+                                int32_t* slot_position, int32_t* token_index,
+                                int32_t* row_assignment, void* stream);
+
+/*
  * out[p, :] = x[token_index[p], :] for p < rows, rows = *num_rows (device
  * int32, e.g. offsets + E from mgg_dispatch_layout) clamped to max_rows, or
  * max_rows when num_rows is null.  Rows of `hidden` BF16/FP16 elements with

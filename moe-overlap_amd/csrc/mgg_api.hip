@@ -23,6 +23,15 @@ namespace mgg {
 constexpr int kCounterSlots = 4096;
 __device__ __align__(256) unsigned long long counter_pool[kCounterSlots];
 
+// Workspace of mgg_dispatch_layout_noalloc: the per-chunk expert histogram
+// (layout_chunks(T * top_k) * E int32, every entry written by the count pass
+// before any pass reads it, so nothing needs clearing), at most
+// kScratchBytes.  Each device holds its own copy for the life of the
+// process; every call on a device shares it, so such calls must not overlap
+// on one device (one stream, or ordered streams).
+constexpr int64_t kScratchBytes = (int64_t)1 << 20;
+__device__ __align__(256) int32_t scratch[kScratchBytes / sizeof(int32_t)];
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -59,6 +68,27 @@ int pool_base(int device, unsigned long long** out) {
     g_slots.base[device] = static_cast<unsigned long long*>(ptr);
   }
   *out = g_slots.base[device];
+  return MGG_OK;
+}
+
+// scratch's device address on the current device, looked up once per device
+// (the array's host-side name is only a stand-in for it).
+std::mutex g_scratch_mu;
+std::vector<int32_t*> g_scratch_ptr;
+
+int scratch_for_current_device(int32_t** out) {
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return hip_error(err, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if ((int)g_scratch_ptr.size() <= device) g_scratch_ptr.resize(device + 1, nullptr);
+  if (g_scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return hip_error(err, "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[device] = static_cast<int32_t*>(ptr);
+  }
+  *out = g_scratch_ptr[device];
   return MGG_OK;
 }
 
@@ -438,6 +468,25 @@ int mgg_dispatch_layout(const void* topk_idx, int idx_type, int64_t num_tokens, 
                                      counts, offsets, slot_position, token_index, row_assignment,
                                      static_cast<int32_t*>(workspace),
                                      static_cast<hipStream_t>(stream));
+}
+
+int mgg_dispatch_layout_noalloc(const void* topk_idx, int idx_type, int64_t num_tokens, int top_k,
+                                int64_t num_experts, int32_t* counts, int32_t* offsets,
+                                int32_t* slot_position, int32_t* token_index,
+                                int32_t* row_assignment, void* stream) {
+  mgg::clear_error();
+  const int64_t need = mgg_dispatch_layout_workspace_bytes(num_tokens, top_k, num_experts);
+  if (need < 0) return set_error(MGG_ERR_INVALID, "sizes must be >= 0");
+  if (need > mgg::kScratchBytes)
+    return set_error(MGG_ERR_UNSUPPORTED,
+                     "mgg_dispatch_layout_noalloc: the layout needs " + std::to_string(need) +
+                         " bytes of workspace (ceil(T*top_k/1024) * E * 4), more than its "
+                         "1 MiB scratch; pass a workspace to mgg_dispatch_layout");
+  int32_t* ws = nullptr;
+  const int rc = mgg::scratch_for_current_device(&ws);
+  if (rc != MGG_OK) return rc;
+  return mgg_dispatch_layout(topk_idx, idx_type, num_tokens, top_k, num_experts, counts, offsets,
+                             slot_position, token_index, row_assignment, ws, need, stream);
 }
 
 int mgg_gather_rows(int dtype, const void* x, int64_t ld_x, const int32_t* token_index,

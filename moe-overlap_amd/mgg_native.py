@@ -83,6 +83,11 @@ _SIGNATURES = {
         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,  # counts, offsets, slot_pos, token_index, row_assign
         _c_ptr, _c_i64, _c_ptr,  # workspace, workspace_bytes, stream
     ],
+    "mgg_dispatch_layout_noalloc": [
+        _c_ptr, _c_i32, _c_i64, _c_i32, _c_i64,  # topk_idx, idx_type, T, top_k, E
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,  # counts, offsets, slot_pos, token_index, row_assign
+        _c_ptr,  # stream
+    ],
     "mgg_gather_rows": [
         _c_i32, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr,
     ],
