@@ -39,6 +39,9 @@
  *   mgg_debug_set_dequeue_counter  -> no counterpart: a test hook (the
  *                                     reference zeroes its counter on the
  *                                     host before each launch, :379-386)
+ *   mgg_debug_set_clock_probe      -> no counterpart: a measurement hook
+ *   mgg_dispatch_layout_noalloc    -> no counterpart: mgg_dispatch_layout
+ *                                     for callers that cannot allocate
  */
 #ifndef MGG_H_
 #define MGG_H_
@@ -223,6 +226,16 @@ int mgg_grouped_gemm_fp8(const void* a, const void* b, void* c, const int32_t* e
  * that the next launch still computes every tile.  Enqueued on `stream`.
  */
 int mgg_debug_set_dequeue_counter(uint64_t value, void* stream);
+
+/*
+ * Measurement hook, no counterpart in the reference: while `probe` (device
+ * memory, two uint64, caller-zeroed) is set, every grouped-GEMM launch adds,
+ * for each workgroup, the shader-clock ticks (s_memtime) and the 100 MHz
+ * reference-clock ticks (s_memrealtime) of its lifetime to probe[0] and
+ * probe[1]; 100 MHz * probe[0] / probe[1] is the average shader clock the
+ * kernel ran at.  Null turns it off (the default).  Process-wide.
+ */
+int mgg_debug_set_clock_probe(uint64_t* probe);
 
 /*
  * Dispatch layout of T tokens routed to top_k experts each (one GPU's share):

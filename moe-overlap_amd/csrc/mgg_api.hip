@@ -37,6 +37,7 @@ namespace {
 thread_local std::string g_last_error;
 
 std::atomic<uint32_t> g_epoch{0};
+std::atomic<unsigned long long*> g_clock_probe{nullptr};
 
 uint32_t next_epoch() {
   uint32_t e = ++g_epoch;
@@ -124,6 +125,8 @@ int counter_for(hipStream_t stream, unsigned long long** out) {
 }
 
 }  // namespace
+
+unsigned long long* clock_probe() { return g_clock_probe.load(); }
 
 int set_error(int code, const std::string& msg) {
   g_last_error = msg;
@@ -367,6 +370,7 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   p.remap_xcd = 1;
   p.report_bm = report_block_m;
   p.report_bn = report_block_n;
+  p.clock_probe = clock_probe();
   if (p.atomic) {
     const int rc = counter_for(st, &p.counter);
     if (rc != MGG_OK) return rc;
@@ -468,6 +472,14 @@ int mgg_dispatch_layout(const void* topk_idx, int idx_type, int64_t num_tokens, 
                                      counts, offsets, slot_position, token_index, row_assignment,
                                      static_cast<int32_t*>(workspace),
                                      static_cast<hipStream_t>(stream));
+}
+
+int mgg_debug_set_clock_probe(uint64_t* probe) {
+  mgg::clear_error();
+  if (probe != nullptr && (reinterpret_cast<uintptr_t>(probe) & 7u) != 0)
+    return set_error(MGG_ERR_INVALID, "probe must be 8-byte aligned");
+  mgg::g_clock_probe.store(reinterpret_cast<unsigned long long*>(probe));
+  return MGG_OK;
 }
 
 int mgg_dispatch_layout_noalloc(const void* topk_idx, int idx_type, int64_t num_tokens, int top_k,

@@ -1224,6 +1224,11 @@ grouped_gemm_kernel(GemmParams p) {
 
   const int G = gridDim.x;
   const int n_tiles = (int)((p.n + BN - 1) / BN);
+  unsigned long long clk0 = 0, ref0 = 0;
+  if (p.clock_probe != nullptr) {
+    clk0 = __builtin_amdgcn_s_memtime();
+    ref0 = __builtin_amdgcn_s_memrealtime();
+  }
 
   // The work_counter's report tile differs from the compute tile when the
   // caller asked for another tile than the one that runs (the queue length it
@@ -1259,6 +1264,12 @@ grouped_gemm_kernel(GemmParams p) {
   run_worker<BM, BN, SBK, NSTAGE, NW, T, EPI>(p, W, w_report, first, n_tiles, s_prefix,
                                          (kOffsLds && p.num_work < 0) ? s_offs : nullptr,
                                          &s_item, lds, s_scale);
+  if (p.clock_probe != nullptr && threadIdx.x == 0) {
+    const unsigned long long clk1 = __builtin_amdgcn_s_memtime();
+    const unsigned long long ref1 = __builtin_amdgcn_s_memrealtime();
+    atomicAdd(p.clock_probe, clk1 - clk0);
+    atomicAdd(p.clock_probe + 1, ref1 - ref0);
+  }
 }
 
 __global__ void fill_u64_kernel(unsigned long long* ptr, int count, unsigned long long value) {

@@ -63,7 +63,14 @@ struct GemmParams {
   // kernel computes with; the kernel counts it from the offsets.
   int32_t report_bm;
   int32_t report_bn;
+  // Measurement hook (null normally): each workgroup adds the shader-clock
+  // ticks (s_memtime) and 100 MHz reference ticks (s_memrealtime) of its
+  // lifetime to [0] and [1].
+  unsigned long long* clock_probe;
 };
+
+// The clock probe buffer set by mgg_debug_set_clock_probe (null: off).
+unsigned long long* clock_probe();
 
 // Launches the grouped GEMM for one (dtype, epilogue, block_m, block_n) on
 // `stream` with `workers` workgroups.  Returns MGG_OK or an error code.

@@ -78,6 +78,7 @@ _SIGNATURES = {
         _c_ptr, _c_i32, _c_i32, _c_ptr,  # work_counter, report_block_m/n, stream
     ],
     "mgg_debug_set_dequeue_counter": [ctypes.c_uint64, _c_ptr],
+    "mgg_debug_set_clock_probe": [_c_ptr],
     "mgg_dispatch_layout": [
         _c_ptr, _c_i32, _c_i64, _c_i32, _c_i64,  # topk_idx, idx_type, T, top_k, E
         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,  # counts, offsets, slot_pos, token_index, row_assign
