@@ -230,10 +230,10 @@ int mgg_debug_set_dequeue_counter(uint64_t value, void* stream);
 /*
  * Measurement hook, no counterpart in the reference: while `probe` (device
  * memory, two uint64, caller-zeroed) is set, every grouped-GEMM launch adds,
- * for each workgroup, the shader-clock ticks (s_memtime) and the 100 MHz
- * reference-clock ticks (s_memrealtime) of its lifetime to probe[0] and
- * probe[1]; 100 MHz * probe[0] / probe[1] is the average shader clock the
- * kernel ran at.  Null turns it off (the default).  Process-wide.
+ * for each of its first eight workgroups, the shader-clock ticks (s_memtime)
+ * of its lifetime to probe[0] and 1 to probe[1]; probe[0] / probe[1] over the
+ * launch time (e.g. from HIP events) is the shader clock the kernel ran at.
+ * Null turns it off (the default).  Process-wide.
  */
 int mgg_debug_set_clock_probe(uint64_t* probe);
 

@@ -1224,11 +1224,14 @@ grouped_gemm_kernel(GemmParams p) {
 
   const int G = gridDim.x;
   const int n_tiles = (int)((p.n + BN - 1) / BN);
-  unsigned long long clk0 = 0, ref0 = 0;
-  if (p.clock_probe != nullptr) {
-    clk0 = __builtin_amdgcn_s_memtime();
-    ref0 = __builtin_amdgcn_s_memrealtime();
-  }
+  // Clock probe: wave 0 of workgroups 0-7 (one per XCD) counts the shader
+  // clock ticks (s_memtime) of its lifetime, which spans the launch; so few
+  // readers and atomics leave the launch they measure unchanged.  (The
+  // 100 MHz reference counter, s_memrealtime, is slow enough to lengthen the
+  // launch, so the caller times the launch with events instead.)
+  const bool probe = p.clock_probe != nullptr && blockIdx.x < 8 && threadIdx.x < 64;
+  unsigned long long clk0 = 0;
+  if (probe) clk0 = __builtin_amdgcn_s_memtime();
 
   // The work_counter's report tile differs from the compute tile when the
   // caller asked for another tile than the one that runs (the queue length it
@@ -1264,11 +1267,12 @@ grouped_gemm_kernel(GemmParams p) {
   run_worker<BM, BN, SBK, NSTAGE, NW, T, EPI>(p, W, w_report, first, n_tiles, s_prefix,
                                          (kOffsLds && p.num_work < 0) ? s_offs : nullptr,
                                          &s_item, lds, s_scale);
-  if (p.clock_probe != nullptr && threadIdx.x == 0) {
+  if (probe) {
     const unsigned long long clk1 = __builtin_amdgcn_s_memtime();
-    const unsigned long long ref1 = __builtin_amdgcn_s_memrealtime();
-    atomicAdd(p.clock_probe, clk1 - clk0);
-    atomicAdd(p.clock_probe + 1, ref1 - ref0);
+    if (threadIdx.x == 0) {
+      atomicAdd(p.clock_probe, clk1 - clk0);
+      atomicAdd(p.clock_probe + 1, 1ull);
+    }
   }
 }
 

@@ -63,9 +63,8 @@ struct GemmParams {
   // kernel computes with; the kernel counts it from the offsets.
   int32_t report_bm;
   int32_t report_bn;
-  // Measurement hook (null normally): each workgroup adds the shader-clock
-  // ticks (s_memtime) and 100 MHz reference ticks (s_memrealtime) of its
-  // lifetime to [0] and [1].
+  // Measurement hook (null normally): workgroups 0-7 add the shader-clock
+  // ticks (s_memtime) of their lifetimes to [0] and 1 each to [1].
   unsigned long long* clock_probe;
 };
 
