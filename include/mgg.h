@@ -40,6 +40,8 @@
  *                                     reference zeroes its counter on the
  *                                     host before each launch, :379-386)
  *   mgg_debug_set_clock_probe      -> no counterpart: a measurement hook
+ *   mgg_debug_set_split_flags      -> no counterpart: a test hook (the
+ *                                     reference never splits a tile)
  *   mgg_dispatch_layout_noalloc    -> no counterpart: mgg_dispatch_layout
  *                                     for callers that cannot allocate
  */
@@ -236,6 +238,17 @@ int mgg_debug_set_dequeue_counter(uint64_t value, void* stream);
  * Null turns it off (the default).  Process-wide.
  */
 int mgg_debug_set_clock_probe(uint64_t* probe);
+
+/*
+ * Test hook, no counterpart in the reference: writes `value` into every
+ * split-tile flag word of atomic launches on `stream` (current device), the
+ * state a launch that did not finish could leave behind.  An atomic launch
+ * whose last round holds at most half as many tiles as workers takes each of
+ * those tiles as two halves of K, which meet through these words.  Fails with
+ * MGG_ERR_INVALID before the stream's first atomic launch (no words yet).
+ * Enqueued on `stream`.
+ */
+int mgg_debug_set_split_flags(uint64_t value, void* stream);
 
 /*
  * Dispatch layout of T tokens routed to top_k experts each (one GPU's share):

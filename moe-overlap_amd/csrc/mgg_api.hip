@@ -2,12 +2,15 @@
 // validation, library-owned dequeue counters, and the launches.  No C++
 // exception crosses this boundary; failures return a status code and leave a
 // message for mgg_last_error().
+#include <algorithm>
 #include <atomic>
 #include <map>
 #include <mutex>
 #include <string>
 #include <utility>
 #include <vector>
+
+#include <hip/hip_ext.h>
 
 #include "mgg.h"
 #include "mgg_internal.h"
@@ -124,6 +127,66 @@ int counter_for(hipStream_t stream, unsigned long long** out) {
   return MGG_OK;
 }
 
+// Split-tile workspaces of the atomic schedule, one per (device, stream):
+// fp32 partial sums in uncached memory (a half written on one XCD is read on
+// another, and no cache level may hold a stale copy) and one zeroed flag word
+// per split tile.  Made on the first atomic launch on a stream that could
+// split, for as many BM x BN slots as it has workers (a split touches at most
+// that many), and replaced by a larger one when a later launch needs more.
+// None is ever freed: uncached memory a kernel has read must stay allocated
+// until the process ends, and a replaced workspace may still be in use by
+// launches queued before it.  A launch under graph capture gets none (it
+// takes every tile whole), so capture never allocates.
+struct SplitSpace {
+  float* partials = nullptr;
+  unsigned long long* flags = nullptr;
+  int64_t bytes = 0;  // of partials
+  int64_t flag_words = 0;
+};
+std::mutex g_split_mu;
+std::map<std::pair<int, hipStream_t>, SplitSpace> g_split;
+
+// Sets p's split fields for a launch of `workers` workgroups of BM x BN
+// tiles on `stream`, or leaves them null when no workspace can be had.
+int split_space_for(hipStream_t stream, int workers, int block_m, int block_n, GemmParams* p) {
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return hip_error(err, "hipGetDevice");
+  if (stream != nullptr) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    err = hipStreamIsCapturing(stream, &capture);
+    if (err != hipSuccess) return hip_error(err, "hipStreamIsCapturing");
+    if (capture != hipStreamCaptureStatusNone) return MGG_OK;
+  }
+  const int64_t slot_bytes = (int64_t)block_m * block_n * 4;
+  const int64_t need_bytes = (int64_t)workers * slot_bytes;
+  const int64_t need_flags = workers / 2 + 1;
+  std::lock_guard<std::mutex> lock(g_split_mu);
+  SplitSpace& sp = g_split[std::make_pair(device, stream)];
+  if (sp.bytes < need_bytes || sp.flag_words < need_flags) {
+    const int64_t bytes = std::max(need_bytes, sp.bytes);
+    const int64_t words = std::max(need_flags, sp.flag_words);
+    void* partials = nullptr;
+    void* flags = nullptr;
+    if (hipExtMallocWithFlags(&partials, (size_t)bytes, hipDeviceMallocUncached) != hipSuccess ||
+        hipMalloc(&flags, (size_t)words * 8) != hipSuccess) {
+      (void)hipGetLastError();  // no workspace: this launch takes every tile whole
+      return MGG_OK;             // (a partial allocation stays unused)
+    }
+    err = hipMemsetAsync(flags, 0, (size_t)words * 8, stream);
+    if (err != hipSuccess) return hip_error(err, "hipMemsetAsync(split flags)");
+    sp.partials = static_cast<float*>(partials);
+    sp.flags = static_cast<unsigned long long*>(flags);
+    sp.bytes = bytes;
+    sp.flag_words = words;
+  }
+  p->split_partials = sp.partials;
+  p->split_flags = sp.flags;
+  const int64_t slots = std::min(sp.bytes / slot_bytes, 2 * (sp.flag_words - 1));
+  p->split_slots = (int32_t)std::min<int64_t>(slots, (int64_t)1 << 30);
+  return MGG_OK;
+}
+
 }  // namespace
 
 unsigned long long* clock_probe() { return g_clock_probe.load(); }
@@ -146,7 +209,7 @@ using mgg::set_error;
 
 extern "C" {
 
-int mgg_abi_version(void) { return 4; }
+int mgg_abi_version(void) { return 5; }
 
 const char* mgg_last_error(void) { return mgg::g_last_error.c_str(); }
 
@@ -372,10 +435,14 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   p.report_bn = report_block_n;
   p.clock_probe = clock_probe();
   if (p.atomic) {
-    const int rc = counter_for(st, &p.counter);
+    int rc = counter_for(st, &p.counter);
     if (rc != MGG_OK) return rc;
     p.epoch = next_epoch();
     p.report = work_counter;
+    if (num_work < 0 && k_size > 0) {
+      rc = split_space_for(st, workers, block_m, block_n, &p);
+      if (rc != MGG_OK) return rc;
+    }
   }
   return launch_grouped_gemm(dtype, epilogue, block_m, block_n, p, workers, st);
 }
@@ -441,6 +508,26 @@ int mgg_debug_set_dequeue_counter(uint64_t value, void* stream) {
   const int rc = mgg::counter_for(st, &word);
   if (rc != MGG_OK) return rc;
   return mgg::launch_fill_u64(word, 1, (unsigned long long)value, st);
+}
+
+int mgg_debug_set_split_flags(uint64_t value, void* stream) {
+  mgg::clear_error();
+  int device = 0;
+  const hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return mgg::hip_error(err, "hipGetDevice");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  unsigned long long* flags = nullptr;
+  int64_t words = 0;
+  {
+    std::lock_guard<std::mutex> lock(mgg::g_split_mu);
+    const auto it = mgg::g_split.find(std::make_pair(device, st));
+    if (it != mgg::g_split.end()) {
+      flags = it->second.flags;
+      words = it->second.flag_words;
+    }
+  }
+  if (flags == nullptr) return set_error(MGG_ERR_INVALID, "no split workspace on this stream yet");
+  return mgg::launch_fill_u64(flags, (int)words, (unsigned long long)value, st);
 }
 
 int64_t mgg_dispatch_layout_workspace_bytes(int64_t num_tokens, int top_k, int64_t num_experts) {

@@ -397,7 +397,7 @@ constexpr bool ablk_mode() {
 // epilogue; in atomic mode the ticket of the next tile is taken early in the
 // current one.  `first` is this worker's first item (a ticket in atomic mode).
 template <int BM, int BN, int SBK, int NSTAGE, int NW, class T, int EPI>
-__device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32_t w_report,
+__device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles, int32_t w_report,
                                            int32_t first, int n_tiles, const int32_t* s_prefix,
                                            const int32_t* s_offs, int32_t* s_item, uint8_t* lds,
                                            float* s_scale) {
@@ -448,6 +448,27 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   const int wn = wave >> 1;
   const int G = gridDim.x;
   const int64_t K = p.k;
+  // ---- split last round (atomic schedule, device-derived queue) ----------
+  // When the tiles past the last full round of G are at most G/2 (and the
+  // library provided the partial-sum workspace), each of them becomes two
+  // work items, K [0, k_half) and [k_half, K), taken by two workers, so the
+  // last round runs on twice as many CUs for half as long.  Queue items past
+  // w_base are the halves (item w_base + 2t + h is half h of tile w_base + t);
+  // W counts work items.  The halves meet in split_fixup.  k_half is a whole
+  // number of A blocks (A-block tile) or stages, so both halves start on a
+  // stage boundary.  The striped schedule keeps whole tiles.
+  constexpr int kGran = kABlk ? 2 * kBK : kBK;
+  const int n_gran = (int)((K + kGran - 1) / kGran);
+  const int k_half = (n_gran / 2) * kGran;
+  int32_t w_base = W_tiles;
+  int32_t W = W_tiles;
+  if (p.atomic && p.num_work < 0 && p.split_flags != nullptr && n_gran >= 4) {
+    const int32_t rem = W_tiles > G ? W_tiles % G : W_tiles;
+    if (rem > 0 && 2 * rem <= G && 2 * rem <= p.split_slots) {
+      w_base = W_tiles - rem;
+      W = W_tiles + rem;
+    }
+  }
   // Atomic schedule: tickets 0 .. W-1 are drawn in all.  Items past the
   // first G take one ticket each (W - G of them when W > G) and every worker
   // with a first item (min(W, G) of them) draws one ticket past the queue
@@ -467,8 +488,11 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
   };
   // K < 2^30 (the host bounds (K+8)*ldb_k*2 below 2^31), so stage positions
   // are 32-bit and the full/partial decision stays in scalar registers.
-  const int k_size = (int)K;
-  const int nk = (int)((K + kBK - 1) / kBK);
+  // K extent of the tile being issued (set by set_sources): all of K, or one
+  // half of it for a split tile.
+  int k_size = (int)K;
+  int nk = (int)((K + kBK - 1) / kBK);
+
   const int64_t last_row = p.m - 1;
 
   // ---- tile decode ---------------------------------------------------------
@@ -480,8 +504,14 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     int64_t row_base;
     int rows_valid;
     int64_t n0;
+    int32_t slot;  // -1: the whole tile; 2t + h: half h of K of split tile t
   };
   auto decode = [&](int32_t item, Coords& c) -> bool {
+    c.slot = -1;
+    if (item >= w_base) {  // a half of a split tile
+      c.slot = item - w_base;
+      item = w_base + (c.slot >> 1);
+    }
     int e, tm, tn;
     if (p.num_work >= 0) {
       e = p.q_expert[item];
@@ -560,17 +590,23 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     int64_t r0 = c.row_base;
     r0 = r0 < 0 ? 0 : (r0 > p.m ? p.m : r0);
     const int64_t r_end = c.row_base + c.rows_valid < p.m ? c.row_base + c.rows_valid : p.m;
-    const int64_t a_end = r0 < r_end ? ((r_end - 1 - r0) * p.lda + K) * kE : 0;
-    a_rsrc = make_rsrc4(a_bytes + r0 * p.lda * kE, a_end);
+    // A split half reads K [kbeg, kend): its descriptors start at kbeg and
+    // end at kend, so every stage offset below is relative to kbeg.
+    const int kb = c.slot < 0 || !(c.slot & 1) ? 0 : k_half;
+    const int klen = c.slot < 0 ? (int)K : (c.slot & 1) ? (int)K - k_half : k_half;
+    k_size = klen;
+    nk = (klen + kBK - 1) / kBK;
+    const int64_t a_end = r0 < r_end ? ((r_end - 1 - r0) * p.lda + klen) * kE : 0;
+    a_rsrc = make_rsrc4(a_bytes + (r0 * p.lda + kb) * kE, a_end);
     if constexpr (T::kBKMajor) {
-      const int64_t b_end = c.n0 < p.n ? ((p.n - 1 - c.n0) * p.ldb_k + K) * kE : 0;
-      b_rsrc = make_rsrc4(b_bytes + ((int64_t)c.e * p.ldb_e + c.n0 * p.ldb_k) * kE, b_end);
+      const int64_t b_end = c.n0 < p.n ? ((p.n - 1 - c.n0) * p.ldb_k + klen) * kE : 0;
+      b_rsrc = make_rsrc4(b_bytes + ((int64_t)c.e * p.ldb_e + c.n0 * p.ldb_k + kb) * kE, b_end);
 #pragma unroll
       for (int t = 0; t < kBPerWave; ++t)
         b_voff[t] = (uint32_t)((b_krow(t) * p.ldb_k + b_kpos(t)) * kE);
     } else {
-      const int64_t b_end = ((K - 1) * p.ldb_k + p.n - c.n0) * 2;
-      b_rsrc = make_rsrc4(b_bytes + ((int64_t)c.e * p.ldb_e + c.n0) * 2, b_end);
+      const int64_t b_end = ((klen - 1) * p.ldb_k + p.n - c.n0) * 2;
+      b_rsrc = make_rsrc4(b_bytes + ((int64_t)c.e * p.ldb_e + c.n0 + kb * p.ldb_k) * 2, b_end);
 #pragma unroll
       for (int t = 0; t < kBPerWave; ++t) {
         const int k = b_krow(t);
@@ -1126,6 +1162,94 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     }
   };
 
+  // ---- split tiles: the halves meet ------------------------------------------
+  // Partial sums of half h of split tile t live in slot 2t + h: wave w's
+  // accumulators as quads of 4 floats, quad g at byte (g * NW + w) * 1024 +
+  // 16 * lane, so each store or load of a wave covers 1 KiB.  They go through
+  // uncached memory with sc0 sc1 (no cache level holds a copy another XCD
+  // could read stale).
+  constexpr int kQuads = kNB * kMB * 4;
+  auto partial_rsrc = [&](int32_t slot) {
+    return __builtin_amdgcn_make_buffer_rsrc(p.split_partials + (int64_t)slot * BM * BN, (short)0,
+                                             BM * BN * 4, 0x00020000);
+  };
+  auto write_partial = [&](const Coords& c) {
+    const auto r = partial_rsrc(c.slot);
+#pragma unroll
+    for (int i = 0; i < kNB; ++i)
+#pragma unroll
+      for (int j = 0; j < kMB; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int g = (i * kMB + j) * 4 + q;
+          // (Elements go through scalars: hipcc miscompiles __builtin_bit_cast
+          // of a vector element, reading element 0 whatever the index.)
+          const u32x4 v = {__float_as_uint(acc[i][j][4 * q]), __float_as_uint(acc[i][j][4 * q + 1]),
+                           __float_as_uint(acc[i][j][4 * q + 2]), __float_as_uint(acc[i][j][4 * q + 3])};
+          __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)(wave * 1024 + 16 * lane), g * NW * 1024, 17);
+        }
+  };
+  // Two 32x32 blocks (8 quads, 32 registers) in flight at a time: the
+  // accumulators leave no room for more.
+  auto add_partial = [&](const Coords& c) {
+    const auto r = partial_rsrc(c.slot ^ 1);
+#pragma unroll
+    for (int b0 = 0; b0 < kNB * kMB; b0 += 2) {
+      u32x4 v[2][4];
+#pragma unroll
+      for (int bb = 0; bb < 2 && b0 + bb < kNB * kMB; ++bb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          v[bb][q] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(wave * 1024 + 16 * lane),
+                                                           ((b0 + bb) * 4 + q) * NW * 1024, 17);
+#pragma unroll
+      for (int bb = 0; bb < 2 && b0 + bb < kNB * kMB; ++bb) {
+        const int i = (b0 + bb) / kMB, j = (b0 + bb) % kMB;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            const uint32_t u = v[bb][q][x];
+            acc[i][j][4 * q + x] += __uint_as_float(u);
+          }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  static_assert(kQuads * 1024 * NW == BM * BN * 4, "a partial slot is the tile's fp32 sums");
+  // After its K loop a half either finds the other half finished (its flag
+  // reads count 1 in this launch's epoch) or writes its partial sums, waits
+  // until they are complete, and takes a ticket on the tile's flag (the
+  // dequeue's epoch-tagged claim, so a flag left by an unfinished launch reads
+  // as fresh).  The half that finds the other finished, or draws ticket 1,
+  // adds the other's partial sums to its accumulators, returns the flag to 0
+  // and stores the tile (returns true); the other stores nothing.  fp32
+  // addition is commutative, so the tile is the same whichever half that is.
+  // No half ever waits for the other.
+  auto split_fixup = [&](const Coords& c) -> bool {
+    unsigned long long* flag = p.split_flags + (c.slot >> 1);
+    if (tid == 0) {
+      const unsigned long long f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_item[1] = ((uint32_t)(f >> 32) == p.epoch && (uint32_t)f == 1u) ? 1 : 0;
+    }
+    __syncthreads();
+    bool last = s_item[1] != 0;
+    __syncthreads();
+    if (!last) {
+      write_partial(c);
+      wait_dma<0>();  // this wave's partial stores are complete (vmcnt counts stores too)
+      __syncthreads();
+      if (tid == 0) s_item[1] = first_ticket(flag, p.epoch) == 1 ? 1 : 0;
+      __syncthreads();
+      last = s_item[1] != 0;
+      __syncthreads();
+    }
+    if (!last) return false;
+    if (tid == 0) __hip_atomic_store(flag, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    add_partial(c);
+    return true;
+  };
+
   // ---- the persistent loop -------------------------------------------------
   // Blocking ticket (used for the first item and to skip a caller queue's
   // invalid items): the leader takes it and broadcasts it through LDS.
@@ -1161,6 +1285,9 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
     if (p.atomic && tid == 0) *s_item = ticket;
     __syncthreads();  // every wave is done reading this tile's LDS stages; s_item is visible
     int32_t next = p.atomic ? *s_item : w + G;
+    // A split half meets the other half before anything of the next item is
+    // issued (fewer registers live across the meeting).
+    const bool store_cur = cur.slot < 0 || split_fixup(cur);
     Coords nxt;
     next = find_valid(next, nxt);
     const bool more = (uint32_t)next < (uint32_t)W;
@@ -1175,7 +1302,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W, int32
       else if (nk > 0)
         issue_stage(issued = 0);
     }
-    epilogue(cur);
+    if (store_cur) epilogue(cur);
     if (!more) break;
     if constexpr (kABlk) {
       for (int st = 1; st < kLB; ++st) issue_bstage(st, 0, kBPerWave);
@@ -1219,7 +1346,7 @@ grouped_gemm_kernel(GemmParams p) {
   __shared__ int32_t s_prefix[kMaxLdsExpertsGemm + 1];
   __shared__ int32_t s_offs[kOffsLds ? kMaxLdsExpertsGemm + 1 : 1];
   __shared__ int32_t s_scan[NT];
-  __shared__ int32_t s_item;
+  __shared__ int32_t s_item[2];  // [0] ticket broadcast, [1] split-tile meeting
   __shared__ float s_scale[T::kScaled ? 2 * (BM + BN) : 1];
 
   const int G = gridDim.x;
@@ -1266,7 +1393,7 @@ grouped_gemm_kernel(GemmParams p) {
   const int32_t first = v;
   run_worker<BM, BN, SBK, NSTAGE, NW, T, EPI>(p, W, w_report, first, n_tiles, s_prefix,
                                          (kOffsLds && p.num_work < 0) ? s_offs : nullptr,
-                                         &s_item, lds, s_scale);
+                                         s_item, lds, s_scale);
   if (probe) {
     const unsigned long long clk1 = __builtin_amdgcn_s_memtime();
     if (threadIdx.x == 0) {

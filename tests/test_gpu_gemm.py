@@ -94,14 +94,21 @@ def test_small_ragged_parity_all_modes(cuda_device, case, dtype):
                 torch.cuda.synchronize()
                 assert_parity(c, a, b, offs, k)
                 outs[(blocks, atomic, queue)] = c
-    # Each tile is computed the same way whatever the schedule: bitwise equal.
+    # A launch that takes every tile whole computes each tile the same way
+    # whatever the schedule or queue: those outputs are bitwise equal.  An
+    # atomic launch with the device-derived queue takes its last round's tiles
+    # in two halves of K when they are at most half the workers (two fp32
+    # partial sums added once: another rounding); it is checked against the
+    # oracle above, and repeats itself bitwise.
     mask = torch.from_numpy(covered_rows(offs)).to(cuda_device)
     for blocks in [(256, 256), (128, 128)]:
         ref = outs[(blocks, False, "device")][: mask.numel()][mask]
-        for atomic in (False, True):
-            for queue in ("device", "prebuilt"):
-                got = outs[(blocks, atomic, queue)][: mask.numel()][mask]
-                assert torch.equal(got, ref), (blocks, atomic, queue)
+        for atomic, queue in ((False, "prebuilt"), (True, "prebuilt")):
+            got = outs[(blocks, atomic, queue)][: mask.numel()][mask]
+            assert torch.equal(got, ref), (blocks, atomic, queue)
+        again = gg.persistent_grouped_gemm(a, b, offs, kernel_tile=blocks, use_atomic_queue=True)
+        assert torch.equal(again[: mask.numel()][mask],
+                           outs[(blocks, True, "device")][: mask.numel()][mask]), blocks
 
 
 # K values around the 256x256 tile's staging: A moves in 64-deep blocks and B
@@ -118,14 +125,18 @@ def test_k_staging_edges_256x256(cuda_device, k, dtype):
     n = 264
     a, b, offs = make_inputs(counts, k, n, dtype, cuda_device, seed=k, extra_rows=5)
     outs = []
-    for atomic in (False, True):
-        log(f"k={k} dtype={dtype} atomic={atomic}")
-        c = gg.persistent_grouped_gemm(a, b, offs, kernel_tile=(256, 256), use_atomic_queue=atomic)
+    for atomic, queue in ((False, "device"), (True, "device"), (True, "prebuilt"), (True, "device")):
+        log(f"k={k} dtype={dtype} atomic={atomic} queue={queue}")
+        c = gg.persistent_grouped_gemm(a, b, offs, kernel_tile=(256, 256), use_atomic_queue=atomic,
+                                       queue=queue)
         torch.cuda.synchronize()
         assert_parity(c, a, b, offs, k)
         outs.append(c)
+    # Whole tiles: bitwise equal across schedules; the atomic device-queue
+    # launch (whose last round may be split in K) repeats itself bitwise.
     mask = torch.from_numpy(covered_rows(offs)).to(cuda_device)
-    assert torch.equal(outs[0][: mask.numel()][mask], outs[1][: mask.numel()][mask])
+    assert torch.equal(outs[0][: mask.numel()][mask], outs[2][: mask.numel()][mask])
+    assert torch.equal(outs[1][: mask.numel()][mask], outs[3][: mask.numel()][mask])
 
 
 def random_case(seed):
@@ -159,8 +170,9 @@ def test_random_shapes_match_oracle(cuda_device, seed):
             torch.cuda.synchronize()
             outs.append(c)
     assert_parity(outs[0], a, b, offs, k)
+    assert_parity(outs[2], a, b, offs, k)  # atomic, device queue: last round maybe split in K
     mask = torch.from_numpy(covered_rows(offs)).to(cuda_device)
-    for c in outs[1:]:
+    for c in (outs[1], outs[3]):  # whole tiles: bitwise equal to the striped device-queue result
         assert torch.equal(c[: mask.numel()][mask], outs[0][: mask.numel()][mask])
 
 
@@ -211,7 +223,10 @@ def test_full_size_configs(cuda_device, name):
     for c in outs:
         err = (c.float() - ref32).abs().max().item()
         assert err <= tol(case.k), err
-    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[2], outs[3])
+    # Striped launches take whole tiles: the same sums whatever the tile shape.
+    assert torch.equal(outs[0], outs[2])
+    if name == "uniform":  # 512 tiles, two full rounds: nothing is split
+        assert torch.equal(outs[0], outs[1]) and torch.equal(outs[2], outs[3])
 
 
 def test_empty_queue_zero_fills_and_keeps_counter(cuda_device):

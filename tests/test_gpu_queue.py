@@ -132,10 +132,12 @@ def test_dirty_counter_word_is_reclaimed(cuda_device, poison):
 
 def test_atomic_launches_on_two_streams_at_once(cuda_device):
     """Atomic launches on two created streams run concurrently on separate
-    counter words; every result matches the serial one bitwise."""
+    counter words and split-tile workspaces; every result matches the serial
+    one bitwise."""
     cases = [make_inputs([300, 5, 0, 600], 256, 512, torch.bfloat16, cuda_device, seed=s)
              for s in (1, 2)]
-    refs = [gg.persistent_grouped_gemm(a, b, o, use_atomic_queue=False) for a, b, o in cases]
+    refs = [gg.persistent_grouped_gemm(a, b, o, num_sms=128 + 64 * i, use_atomic_queue=True)
+            for i, (a, b, o) in enumerate(cases)]
     streams = [torch.cuda.Stream(device=cuda_device) for _ in cases]
     torch.cuda.synchronize()
     outs = [[], []]

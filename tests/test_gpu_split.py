@@ -1,0 +1,151 @@
+"""GPU tests of the atomic schedule's split last round.
+
+With the device-derived queue, an atomic launch whose last round holds at most
+half as many tiles as there are workers takes each of those tiles as two
+halves of K on two workers: each half writes its fp32 partial sums, and the
+half that finishes second adds the other's and stores the tile.  Checked here:
+parity with the oracle (tolerance as in test_gpu_gemm), a repeated launch
+giving the same bits (the sum of the two halves does not depend on which
+finishes first), the work_counter's W + G, flag words left at any value by an
+unfinished launch, and the fused-epilogue, K-major and fp8 variants.  The
+reference never splits a tile (src/triton_grouped_gemm.py:157-233 takes whole
+items); results agree with it within the tolerance, not bitwise.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import grouped_gemm as gg
+import mgg_native as nat
+from oracle import grouped_gemm_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def tol(k):
+    return 2e-2 * math.sqrt(max(k, 512) / 512)
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_inputs(counts, k, n, dtype, device, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    a = torch.randn(int(sum(counts)), k, generator=gen).to(dtype)
+    b = (torch.randn(len(counts), k, n, generator=gen) / math.sqrt(k)).to(dtype)
+    offs = torch.tensor(orc.expert_offsets_from_recv_counts(counts), dtype=torch.int32)
+    return a.to(device), b.to(device), offs.to(device)
+
+
+def assert_parity(c, a, b, offs, k):
+    want = orc.grouped_gemm(a.float().cpu().numpy(), b.float().cpu().numpy(), offs.cpu().numpy(),
+                            acc_dtype=np.float64)
+    err = float(np.abs(c.float().cpu().numpy() - want).max())
+    assert err <= tol(k), f"max abs err {err} > {tol(k)}"
+
+
+def tiles(counts, n, bm, bn):
+    return sum((c + bm - 1) // bm for c in counts if c > 0) * ((n + bn - 1) // bn)
+
+
+def splits(w, g):
+    """Tiles the atomic schedule takes in halves (K long enough)."""
+    rem = w % g if w > g else w
+    return rem if 0 < rem and 2 * rem <= g else 0
+
+
+# (counts, K, N, workers): 24 tiles of 256x256 on 256 workers (all split), on
+# 20 (4 tiles past the full round, split), 7 (3 split), 30 (24 > 15: whole).
+CASES = [([300, 0, 257, 1, 600], 1032, 520, 256),
+         ([300, 0, 257, 1, 600], 1032, 520, 20),
+         ([300, 0, 257, 1, 600], 1032, 520, 7),
+         ([300, 0, 257, 1, 600], 1032, 520, 30),
+         ([64] * 3, 264, 256, 256)]  # K = 264: halves of 128 and 136 (a partial stage)
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_split_last_round(cuda_device, case, dtype):
+    counts, k, n, g = CASES[case]
+    a, b, offs = make_inputs(counts, k, n, dtype, cuda_device, seed=case)
+    w = tiles(counts, n, 256, 256)
+    log(f"split case={case} W={w} G={g} split tiles={splits(w, g)} dtype={dtype}")
+    counter = torch.zeros(1, dtype=torch.int32, device=cuda_device)
+    c = gg.persistent_grouped_gemm(a, b, offs, num_sms=g, block_m=256, block_n=256,
+                                   work_counter=counter)
+    torch.cuda.synchronize()
+    assert counter.item() == w + g  # the reference's count for the requested tile
+    assert_parity(c, a, b, offs, k)
+    for rep in range(3):
+        again = gg.persistent_grouped_gemm(a, b, offs, num_sms=g)
+        torch.cuda.synchronize()
+        assert torch.equal(again, c), rep
+    whole = gg.persistent_grouped_gemm(a, b, offs, num_sms=g, use_atomic_queue=False)
+    torch.cuda.synchronize()
+    if splits(w, g) == 0:
+        assert torch.equal(whole, c)
+    elif case == 0:  # 24 split tiles of random sums: some output rounds differently
+        assert not torch.equal(whole, c)
+
+
+@pytest.mark.parametrize("poison", [0xFFFFFFFFFFFFFFFF, 0x0000000100000001, 0x7FFFFFFF00000001,
+                                    0x0000000000000005])
+def test_split_flags_left_dirty(cuda_device, poison):
+    """Flag words left at any value (as a launch that did not finish could
+    leave them) neither lose a half's partial sums nor add them twice."""
+    counts, k, n = [300, 0, 257, 1, 600], 1032, 520
+    a, b, offs = make_inputs(counts, k, n, torch.bfloat16, cuda_device, seed=3)
+    stream = torch.cuda.current_stream().cuda_stream
+    clean = gg.persistent_grouped_gemm(a, b, offs)  # also creates this stream's split workspace
+    torch.cuda.synchronize()
+    assert_parity(clean, a, b, offs, k)
+    for rep in range(2):
+        nat.check(nat.lib().mgg_debug_set_split_flags(poison, stream))
+        got = gg.persistent_grouped_gemm(a, b, offs)
+        torch.cuda.synchronize()
+        log(f"poison={poison:#x} rep={rep}")
+        assert torch.equal(got, clean), rep
+
+
+def test_split_kmajor_b_matches_nmajor(cuda_device):
+    """K-major B (a [E, K, N] view of [E, N, K] memory) splits at the same K
+    and gives the same bits as N-major B."""
+    counts, k, n = [300, 0, 257, 1, 600], 1032, 520
+    a, b, offs = make_inputs(counts, k, n, torch.bfloat16, cuda_device, seed=4)
+    b_km = b.transpose(1, 2).contiguous().transpose(1, 2)
+    for tile in ((256, 256), (128, 128)):
+        c_n = gg.persistent_grouped_gemm(a, b, offs, kernel_tile=tile)
+        c_k = gg.persistent_grouped_gemm(a, b_km, offs, kernel_tile=tile)
+        torch.cuda.synchronize()
+        assert_parity(c_k, a, b, offs, k)
+        assert torch.equal(c_k, c_n), tile
+
+
+def test_split_fp8(cuda_device):
+    """fp8: both halves' sums are unscaled; the second half applies the row
+    and column scales once, after adding them."""
+    counts, k, n = [300, 5, 0, 600], 1024, 384
+    gen = torch.Generator().manual_seed(11)
+    x = torch.randn(sum(counts), k, generator=gen)
+    wt = torch.randn(len(counts), n, k, generator=gen) / math.sqrt(k)
+    a, sa = gg.quantize_fp8_rows(x)
+    b, sb = gg.quantize_fp8_rows(wt)
+    offs = torch.tensor(orc.expert_offsets_from_recv_counts(counts), dtype=torch.int32)
+    a, sa, b, sb, offs = (t.to(cuda_device) for t in (a, sa, b, sb, offs))
+    ref = orc.grouped_gemm_fp8(a.cpu().view(torch.uint8).numpy(), b.cpu().view(torch.uint8).numpy(),
+                               offs.cpu().numpy(), sa.cpu().numpy(), sb.cpu().numpy())
+    mag = orc.grouped_gemm_fp8(a.cpu().view(torch.uint8).numpy(), b.cpu().view(torch.uint8).numpy(),
+                               offs.cpu().numpy(), sa.cpu().numpy(), sb.cpu().numpy(), magnitude=True)
+    outs = []
+    for rep in range(2):
+        c = gg.persistent_grouped_gemm(a, b.transpose(1, 2), offs, a_scale=sa, b_scale=sb,
+                                       kernel_tile=(256, 256))
+        torch.cuda.synchronize()
+        got = c.float().cpu().numpy()
+        assert np.all(np.abs(got - ref) <= 2 ** -8 * np.abs(ref) + 2 ** -16 * mag)
+        outs.append(c)
+    assert torch.equal(outs[0], outs[1])
