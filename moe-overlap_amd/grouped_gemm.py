@@ -34,6 +34,12 @@ Differences, all in arguments that do not change results:
   the reference leaves there, while the dequeue itself runs on a
   library-owned per-stream counter word, so no separate zeroing launch is
   needed.
+* The atomic schedule with the device-derived queue takes a last round of
+  at most half as many tiles as workers as two halves of K per tile, added
+  once in fp32 by whichever half finishes second: the output can differ in
+  the last bits from the striped schedule's (both within the tolerance of
+  the fp32 product; each repeats itself bitwise).  Graph-captured launches
+  and prebuilt queues take whole tiles.
 * Operands whose inner stride is not 1, whose rows are not 16-byte aligned, or
   with K or N not a multiple of 8, are copied (and zero-padded) on the device
   first.  K == 0 gives zeros, as there.
