@@ -136,7 +136,10 @@ int counter_for(hipStream_t stream, unsigned long long** out) {
 // None is ever freed: uncached memory a kernel has read must stay allocated
 // until the process ends, and a replaced workspace may still be in use by
 // launches queued before it.  A launch under graph capture gets none (it
-// takes every tile whole), so capture never allocates.
+// takes every tile whole), so capture never allocates.  At most
+// kMaxSplitSpaces streams per device get one (64 MiB each at 256 workers of
+// 256x256 tiles); launches on further streams take every tile whole.
+constexpr int kMaxSplitSpaces = 16;
 struct SplitSpace {
   float* partials = nullptr;
   unsigned long long* flags = nullptr;
@@ -162,7 +165,13 @@ int split_space_for(hipStream_t stream, int workers, int block_m, int block_n, G
   const int64_t need_bytes = (int64_t)workers * slot_bytes;
   const int64_t need_flags = workers / 2 + 1;
   std::lock_guard<std::mutex> lock(g_split_mu);
-  SplitSpace& sp = g_split[std::make_pair(device, stream)];
+  const auto key = std::make_pair(device, stream);
+  if (g_split.find(key) == g_split.end()) {
+    int on_device = 0;
+    for (const auto& kv : g_split) on_device += kv.first.first == device ? 1 : 0;
+    if (on_device >= kMaxSplitSpaces) return MGG_OK;
+  }
+  SplitSpace& sp = g_split[key];
   if (sp.bytes < need_bytes || sp.flag_words < need_flags) {
     const int64_t bytes = std::max(need_bytes, sp.bytes);
     const int64_t words = std::max(need_flags, sp.flag_words);
