@@ -243,8 +243,9 @@ int mgg_debug_set_clock_probe(uint64_t* probe);
  * Test hook, no counterpart in the reference: writes `value` into every
  * split-tile flag word of atomic launches on `stream` (current device), the
  * state a launch that did not finish could leave behind.  An atomic launch
- * whose last round holds at most half as many tiles as workers takes each of
- * those tiles as two halves of K, which meet through these words.  Fails with
+ * whose last round holds at most a quarter (a half) as many tiles as workers
+ * takes each of those tiles as 4 (2) parts of K, which meet pairwise through
+ * these words.  Fails with
  * MGG_ERR_INVALID before the stream's first atomic launch (no words yet).
  * Enqueued on `stream`.
  */

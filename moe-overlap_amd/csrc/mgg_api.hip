@@ -128,11 +128,13 @@ int counter_for(hipStream_t stream, unsigned long long** out) {
 }
 
 // Split-tile workspaces of the atomic schedule, one per (device, stream):
-// fp32 partial sums in uncached memory (a half written on one XCD is read on
-// another, and no cache level may hold a stale copy) and one zeroed flag word
-// per split tile.  Made on the first atomic launch on a stream that could
-// split, for as many BM x BN slots as it has workers (a split touches at most
-// that many), and replaced by a larger one when a later launch needs more.
+// fp32 partial sums in uncached memory (a part written on one XCD is read on
+// another, and no cache level may hold a stale copy) and zeroed flag words,
+// one slot and one flag word per work item of a split tile (a tile of s parts
+// uses s slots and s - 1 flags).  Made on the first atomic launch on a stream
+// that could split, for as many BM x BN slots as it has workers (a split
+// touches at most that many), and replaced by a larger one when a later
+// launch needs more.
 // None is ever freed: uncached memory a kernel has read must stay allocated
 // until the process ends, and a replaced workspace may still be in use by
 // launches queued before it.  A launch under graph capture gets none (it
@@ -163,7 +165,7 @@ int split_space_for(hipStream_t stream, int workers, int block_m, int block_n, G
   }
   const int64_t slot_bytes = (int64_t)block_m * block_n * 4;
   const int64_t need_bytes = (int64_t)workers * slot_bytes;
-  const int64_t need_flags = workers / 2 + 1;
+  const int64_t need_flags = workers;
   std::lock_guard<std::mutex> lock(g_split_mu);
   const auto key = std::make_pair(device, stream);
   if (g_split.find(key) == g_split.end()) {
@@ -191,7 +193,7 @@ int split_space_for(hipStream_t stream, int workers, int block_m, int block_n, G
   }
   p->split_partials = sp.partials;
   p->split_flags = sp.flags;
-  const int64_t slots = std::min(sp.bytes / slot_bytes, 2 * (sp.flag_words - 1));
+  const int64_t slots = std::min(sp.bytes / slot_bytes, sp.flag_words);
   p->split_slots = (int32_t)std::min<int64_t>(slots, (int64_t)1 << 30);
   return MGG_OK;
 }

@@ -49,6 +49,10 @@
 #ifndef MGG_FP8_NW
 #define MGG_FP8_NW 8
 #endif
+// Most parts a tile of a short last round is split into: 1 << MGG_SPLIT_MAX_LOG.
+#ifndef MGG_SPLIT_MAX_LOG
+#define MGG_SPLIT_MAX_LOG 2
+#endif
 
 namespace mgg {
 namespace {
@@ -449,24 +453,29 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   const int G = gridDim.x;
   const int64_t K = p.k;
   // ---- split last round (atomic schedule, device-derived queue) ----------
-  // When the tiles past the last full round of G are at most G/2 (and the
-  // library provided the partial-sum workspace), each of them becomes two
-  // work items, K [0, k_half) and [k_half, K), taken by two workers, so the
-  // last round runs on twice as many CUs for half as long.  Queue items past
-  // w_base are the halves (item w_base + 2t + h is half h of tile w_base + t);
-  // W counts work items.  The halves meet in split_fixup.  k_half is a whole
-  // number of A blocks (A-block tile) or stages, so both halves start on a
-  // stage boundary.  The striped schedule keeps whole tiles.
+  // When the tiles past the last full round of G are at most G/s for s = 4
+  // or 2 (and the library provided the partial-sum workspace), each of them
+  // becomes s work items, the parts q = 0 .. s-1 of K, [K_q, K_q+1) with
+  // K_q = floor(q * n_gran / s) granules, taken by s workers: the last round
+  // runs on s times as many CUs for 1/s as long.  Queue items past w_base
+  // are the parts (item w_base + s*t + q is part q of tile w_base + t); W
+  // counts work items.  The parts meet pairwise in split_fixup.  A granule
+  // is an A block (A-block tile) or a stage, so every part starts on a stage
+  // boundary; each part holds at least two.  The striped schedule keeps
+  // whole tiles.
   constexpr int kGran = kABlk ? 2 * kBK : kBK;
   const int n_gran = (int)((K + kGran - 1) / kGran);
-  const int k_half = (n_gran / 2) * kGran;
   int32_t w_base = W_tiles;
   int32_t W = W_tiles;
-  if (p.atomic && p.num_work < 0 && p.split_flags != nullptr && n_gran >= 4) {
+  int split_log = 0;  // s = 1 << split_log parts per split tile
+  if (p.atomic && p.num_work < 0 && p.split_flags != nullptr) {
     const int32_t rem = W_tiles > G ? W_tiles % G : W_tiles;
-    if (rem > 0 && 2 * rem <= G && 2 * rem <= p.split_slots) {
+    for (int l = MGG_SPLIT_MAX_LOG; l >= 1 && split_log == 0; --l)
+      if (rem > 0 && (rem << l) <= G && (rem << l) <= p.split_slots && n_gran >= (2 << l))
+        split_log = l;
+    if (split_log > 0) {
       w_base = W_tiles - rem;
-      W = W_tiles + rem;
+      W = w_base + (rem << split_log);
     }
   }
   // Atomic schedule: tickets 0 .. W-1 are drawn in all.  Items past the
@@ -504,13 +513,13 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     int64_t row_base;
     int rows_valid;
     int64_t n0;
-    int32_t slot;  // -1: the whole tile; 2t + h: half h of K of split tile t
+    int32_t slot;  // -1: the whole tile; s*t + q: part q of K of split tile t
   };
   auto decode = [&](int32_t item, Coords& c) -> bool {
     c.slot = -1;
-    if (item >= w_base) {  // a half of a split tile
+    if (item >= w_base) {  // a part of a split tile
       c.slot = item - w_base;
-      item = w_base + (c.slot >> 1);
+      item = w_base + (c.slot >> split_log);
     }
     int e, tm, tn;
     if (p.num_work >= 0) {
@@ -590,10 +599,15 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     int64_t r0 = c.row_base;
     r0 = r0 < 0 ? 0 : (r0 > p.m ? p.m : r0);
     const int64_t r_end = c.row_base + c.rows_valid < p.m ? c.row_base + c.rows_valid : p.m;
-    // A split half reads K [kbeg, kend): its descriptors start at kbeg and
-    // end at kend, so every stage offset below is relative to kbeg.
-    const int kb = c.slot < 0 || !(c.slot & 1) ? 0 : k_half;
-    const int klen = c.slot < 0 ? (int)K : (c.slot & 1) ? (int)K - k_half : k_half;
+    // A split part reads K [kb, ke): its descriptors start at kb and end at
+    // ke, so every stage offset below is relative to kb.
+    int kb = 0, klen = (int)K;
+    if (c.slot >= 0) {
+      const int q = c.slot & ((1 << split_log) - 1);
+      kb = ((q * n_gran) >> split_log) * kGran;
+      const int ke = q == (1 << split_log) - 1 ? (int)K : (((q + 1) * n_gran) >> split_log) * kGran;
+      klen = ke - kb;
+    }
     k_size = klen;
     nk = (klen + kBK - 1) / kBK;
     const int64_t a_end = r0 < r_end ? ((r_end - 1 - r0) * p.lda + klen) * kE : 0;
@@ -1162,8 +1176,8 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     }
   };
 
-  // ---- split tiles: the halves meet ------------------------------------------
-  // Partial sums of half h of split tile t live in slot 2t + h: wave w's
+  // ---- split tiles: the parts meet -------------------------------------------
+  // A slot holds one part's (or a subtree's) partial sums: wave w's
   // accumulators as quads of 4 floats, quad g at byte (g * NW + w) * 1024 +
   // 16 * lane, so each store or load of a wave covers 1 KiB.  They go through
   // uncached memory with sc0 sc1 (no cache level holds a copy another XCD
@@ -1173,8 +1187,8 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     return __builtin_amdgcn_make_buffer_rsrc(p.split_partials + (int64_t)slot * BM * BN, (short)0,
                                              BM * BN * 4, 0x00020000);
   };
-  auto write_partial = [&](const Coords& c) {
-    const auto r = partial_rsrc(c.slot);
+  auto write_partial = [&](int32_t slot) {
+    const auto r = partial_rsrc(slot);
 #pragma unroll
     for (int i = 0; i < kNB; ++i)
 #pragma unroll
@@ -1191,8 +1205,8 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   };
   // Two 32x32 blocks (8 quads, 32 registers) in flight at a time: the
   // accumulators leave no room for more.
-  auto add_partial = [&](const Coords& c) {
-    const auto r = partial_rsrc(c.slot ^ 1);
+  auto add_partial = [&](int32_t slot) {
+    const auto r = partial_rsrc(slot);
 #pragma unroll
     for (int b0 = 0; b0 < kNB * kMB; b0 += 2) {
       u32x4 v[2][4];
@@ -1217,36 +1231,48 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     }
   };
   static_assert(kQuads * 1024 * NW == BM * BN * 4, "a partial slot is the tile's fp32 sums");
-  // After its K loop a half either finds the other half finished (its flag
-  // reads count 1 in this launch's epoch) or writes its partial sums, waits
-  // until they are complete, and takes a ticket on the tile's flag (the
-  // dequeue's epoch-tagged claim, so a flag left by an unfinished launch reads
-  // as fresh).  The half that finds the other finished, or draws ticket 1,
-  // adds the other's partial sums to its accumulators, returns the flag to 0
-  // and stores the tile (returns true); the other stores nothing.  fp32
-  // addition is commutative, so the tile is the same whichever half that is.
-  // No half ever waits for the other.
+  // The s parts of a split tile meet in a binary tree of s - 1 meetings.  At
+  // level l a worker holds the sum of the 2^l parts from b = q & -2^l (its
+  // accumulators), and meets the holder of the sibling subtree b ^ 2^l on
+  // the level's flag word for the pair.  It either finds the sibling
+  // finished (the flag reads count 1 in this launch's epoch) or writes its
+  // sums to slot s*t + b, waits until they are complete, and takes a ticket
+  // on the flag (the dequeue's epoch-tagged claim, so a flag left by an
+  // unfinished launch reads as fresh).  The worker that finds the sibling
+  // finished, or draws ticket 1, returns the flag to 0, adds the sibling's
+  // sums from slot s*t + (b ^ 2^l) and goes on to the next level; the other
+  // is done.  The worker that completes the last level stores the tile
+  // (returns true).  fp32 addition is commutative, so every meeting's sum,
+  // and the tile, is the same whichever worker arrives first, and no worker
+  // ever waits for another.  Flag words of tile t: s*t + (s - (s >> l)) +
+  // (q >> (l + 1)) at level l.
   auto split_fixup = [&](const Coords& c) -> bool {
-    unsigned long long* flag = p.split_flags + (c.slot >> 1);
-    if (tid == 0) {
-      const unsigned long long f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_item[1] = ((uint32_t)(f >> 32) == p.epoch && (uint32_t)f == 1u) ? 1 : 0;
+    const int s = 1 << split_log;
+    const int32_t t = c.slot >> split_log;
+    const int q = c.slot & (s - 1);
+    for (int l = 0; l < split_log; ++l) {
+      unsigned long long* flag = p.split_flags + (int64_t)s * t + (s - (s >> l)) + (q >> (l + 1));
+      const int32_t b = q & -(1 << l);
+      if (tid == 0) {
+        const unsigned long long f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_item[1] = ((uint32_t)(f >> 32) == p.epoch && (uint32_t)f == 1u) ? 1 : 0;
+      }
+      __syncthreads();
+      bool last = s_item[1] != 0;
+      __syncthreads();
+      if (!last) {
+        write_partial(s * t + b);
+        wait_dma<0>();  // this wave's partial stores are complete (vmcnt counts stores too)
+        __syncthreads();
+        if (tid == 0) s_item[1] = first_ticket(flag, p.epoch) == 1 ? 1 : 0;
+        __syncthreads();
+        last = s_item[1] != 0;
+        __syncthreads();
+      }
+      if (!last) return false;
+      if (tid == 0) __hip_atomic_store(flag, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      add_partial(s * t + (b ^ (1 << l)));
     }
-    __syncthreads();
-    bool last = s_item[1] != 0;
-    __syncthreads();
-    if (!last) {
-      write_partial(c);
-      wait_dma<0>();  // this wave's partial stores are complete (vmcnt counts stores too)
-      __syncthreads();
-      if (tid == 0) s_item[1] = first_ticket(flag, p.epoch) == 1 ? 1 : 0;
-      __syncthreads();
-      last = s_item[1] != 0;
-      __syncthreads();
-    }
-    if (!last) return false;
-    if (tid == 0) __hip_atomic_store(flag, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    add_partial(c);
     return true;
   };
 
@@ -1285,8 +1311,8 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     if (p.atomic && tid == 0) *s_item = ticket;
     __syncthreads();  // every wave is done reading this tile's LDS stages; s_item is visible
     int32_t next = p.atomic ? *s_item : w + G;
-    // A split half meets the other half before anything of the next item is
-    // issued (fewer registers live across the meeting).
+    // A split part meets the others before anything of the next item is
+    // issued (fewer registers live across the meetings).
     const bool store_cur = cur.slot < 0 || split_fixup(cur);
     Coords nxt;
     next = find_valid(next, nxt);

@@ -67,11 +67,11 @@ struct GemmParams {
   // ticks (s_memtime) of their lifetimes to [0] and 1 each to [1].
   unsigned long long* clock_probe;
   // Atomic schedule with the device-derived queue: when the last round holds
-  // at most half as many tiles as there are workers, each of those tiles is
-  // taken as two halves of K by two workers (null: never).  split_partials
-  // holds split_slots BM x BN fp32 partial sums (uncached memory, so every
-  // XCD reads what another wrote); split_flags one (epoch << 32 | count)
-  // word per split tile, split_slots / 2 of them.
+  // at most a half (a quarter) as many tiles as there are workers, each of
+  // those tiles is taken as 2 (4) parts of K by as many workers (null:
+  // never).  split_partials holds split_slots BM x BN fp32 partial sums
+  // (uncached memory, so every XCD reads what another wrote); split_flags
+  // split_slots (epoch << 32 | count) words, s - 1 per tile of s parts.
   float* split_partials;
   unsigned long long* split_flags;
   int32_t split_slots;

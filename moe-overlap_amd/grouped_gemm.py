@@ -35,9 +35,9 @@ Differences, all in arguments that do not change results:
   library-owned per-stream counter word, so no separate zeroing launch is
   needed.
 * The atomic schedule with the device-derived queue takes a last round of
-  at most half as many tiles as workers as two halves of K per tile, added
-  once in fp32 by whichever half finishes second: the output can differ in
-  the last bits from the striped schedule's (both within the tolerance of
+  at most a quarter (a half) as many tiles as workers as 4 (2) parts of K per
+  tile, their fp32 sums added pairwise in a fixed tree: the output can differ
+  in the last bits from the striped schedule's (both within the tolerance of
   the fp32 product; each repeats itself bitwise).  Graph-captured launches
   and prebuilt queues take whole tiles.
 * Operands whose inner stride is not 1, whose rows are not 16-byte aligned, or

@@ -1,15 +1,16 @@
 """GPU tests of the atomic schedule's split last round.
 
 With the device-derived queue, an atomic launch whose last round holds at most
-half as many tiles as there are workers takes each of those tiles as two
-halves of K on two workers: each half writes its fp32 partial sums, and the
-half that finishes second adds the other's and stores the tile.  Checked here:
-parity with the oracle (tolerance as in test_gpu_gemm), a repeated launch
-giving the same bits (the sum of the two halves does not depend on which
-finishes first), the work_counter's W + G, flag words left at any value by an
-unfinished launch, and the fused-epilogue, K-major and fp8 variants.  The
-reference never splits a tile (src/triton_grouped_gemm.py:157-233 takes whole
-items); results agree with it within the tolerance, not bitwise.
+a quarter (a half) as many tiles as there are workers takes each of those
+tiles as 4 (2) parts of K on as many workers.  The parts meet pairwise in a
+binary tree: at each meeting the worker that arrives first writes its fp32
+partial sums and the other adds them and goes on; the last meeting's winner
+stores the tile.  Checked here: parity with the oracle (tolerance as in
+test_gpu_gemm), a repeated launch giving the same bits (each meeting's sum does
+not depend on which worker arrives first), the work_counter's W + G, flag
+words left at any value by an unfinished launch, and the K-major and fp8
+variants.  The reference never splits a tile (src/triton_grouped_gemm.py:157-233
+takes whole items); results agree with it within the tolerance, not bitwise.
 """
 import math
 import sys
@@ -52,19 +53,29 @@ def tiles(counts, n, bm, bn):
     return sum((c + bm - 1) // bm for c in counts if c > 0) * ((n + bn - 1) // bn)
 
 
-def splits(w, g):
-    """Tiles the atomic schedule takes in halves (K long enough)."""
+def split_parts(w, g, k, gran=64):
+    """(tiles split, parts per tile) of the atomic schedule's last round: the
+    most parts s in (4, 2) with s * rem <= g and at least two K granules
+    (64-deep A blocks of the 256x256 tile) per part."""
     rem = w % g if w > g else w
-    return rem if 0 < rem and 2 * rem <= g else 0
+    n_gran = -(-k // gran)
+    for s in (4, 2):
+        if 0 < rem and s * rem <= g and n_gran >= 2 * s:
+            return rem, s
+    return 0, 1
 
 
-# (counts, K, N, workers): 24 tiles of 256x256 on 256 workers (all split), on
-# 20 (4 tiles past the full round, split), 7 (3 split), 30 (24 > 15: whole).
+# (counts, K, N, workers): 24 tiles of 256x256 on 256 workers (all split in
+# 4), on 20 (4 tiles past the full round, in 4), 7 (3 tiles in 2), 30 (24 >
+# 15: whole); K = 264: 3 tiles in halves of 128 and 136 (a partial stage);
+# K = 520: 3 tiles in quarters of 128, 128, 128 and 136.
 CASES = [([300, 0, 257, 1, 600], 1032, 520, 256),
          ([300, 0, 257, 1, 600], 1032, 520, 20),
          ([300, 0, 257, 1, 600], 1032, 520, 7),
          ([300, 0, 257, 1, 600], 1032, 520, 30),
-         ([64] * 3, 264, 256, 256)]  # K = 264: halves of 128 and 136 (a partial stage)
+         ([64] * 3, 264, 256, 256),
+         ([64] * 3, 520, 256, 256)]
+EXPECT_PARTS = [4, 4, 2, 1, 2, 4]
 
 
 @pytest.mark.parametrize("case", range(len(CASES)))
@@ -73,7 +84,9 @@ def test_split_last_round(cuda_device, case, dtype):
     counts, k, n, g = CASES[case]
     a, b, offs = make_inputs(counts, k, n, dtype, cuda_device, seed=case)
     w = tiles(counts, n, 256, 256)
-    log(f"split case={case} W={w} G={g} split tiles={splits(w, g)} dtype={dtype}")
+    n_split, parts = split_parts(w, g, k)
+    assert parts == EXPECT_PARTS[case]
+    log(f"split case={case} W={w} G={g} split tiles={n_split} parts={parts} dtype={dtype}")
     counter = torch.zeros(1, dtype=torch.int32, device=cuda_device)
     c = gg.persistent_grouped_gemm(a, b, offs, num_sms=g, block_m=256, block_n=256,
                                    work_counter=counter)
@@ -86,7 +99,7 @@ def test_split_last_round(cuda_device, case, dtype):
         assert torch.equal(again, c), rep
     whole = gg.persistent_grouped_gemm(a, b, offs, num_sms=g, use_atomic_queue=False)
     torch.cuda.synchronize()
-    if splits(w, g) == 0:
+    if n_split == 0:
         assert torch.equal(whole, c)
     elif case == 0:  # 24 split tiles of random sums: some output rounds differently
         assert not torch.equal(whole, c)
@@ -126,8 +139,9 @@ def test_split_kmajor_b_matches_nmajor(cuda_device):
 
 
 def test_split_fp8(cuda_device):
-    """fp8: both halves' sums are unscaled; the second half applies the row
-    and column scales once, after adding them."""
+    """fp8 (12 tiles of 256x256, K = 1024: quarters of two 128-deep stages):
+    the parts' sums are unscaled; the worker that completes the last meeting
+    applies the row and column scales once, after adding them."""
     counts, k, n = [300, 5, 0, 600], 1024, 384
     gen = torch.Generator().manual_seed(11)
     x = torch.randn(sum(counts), k, generator=gen)
