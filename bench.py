@@ -200,8 +200,10 @@ def recorded_traffic(mode, workload, kernel_tile):
 
 def expert_mlp_summary(dev, steps: int = 20):
     """The benchmark expert-MLP config (8192 tokens top-2 of 16, H 2048, SwiGLU
-    F 4096): whole forward (layout, gather, up GEMM + SwiGLU, down GEMM,
-    combine) and each launch alone, from HIP events on the current stream."""
+    F 4096): whole forward (layout, up GEMM with the gather fused + SwiGLU,
+    down GEMM, combine) and each launch alone, from HIP events on the current
+    stream; also the separate gather and plain up GEMM the fused launch
+    replaces."""
     import torch
 
     import expert_mlp as mlp
@@ -220,9 +222,11 @@ def expert_mlp_summary(dev, steps: int = 20):
     y = mlp._grouped_gemm_ex(h, case.w2, lay.offsets, mlp._EPILOGUES["none"], case.hidden, None, 256, True)
     parts = {
         "dispatch_layout": lambda: mlp.dispatch_layout(case.topk_idx, case.experts),
-        "gather": lambda: mlp.permute_tokens(case.x, lay),
-        "up_gemm_swiglu": lambda: mlp._grouped_gemm_ex(xp, w1, lay.offsets, mlp._EPILOGUES["swiglu"],
-                                                      case.ffn, None, 256, True),
+        "up_gemm_gathered_swiglu": lambda: mlp._grouped_gemm_gathered(
+            case.x, lay, w1, mlp._EPILOGUES["swiglu"], case.ffn, None, True),
+        "gather_unfused": lambda: mlp.permute_tokens(case.x, lay),
+        "up_gemm_swiglu_unfused": lambda: mlp._grouped_gemm_ex(
+            xp, w1, lay.offsets, mlp._EPILOGUES["swiglu"], case.ffn, None, 256, True),
         "down_gemm": lambda: mlp._grouped_gemm_ex(h, case.w2, lay.offsets, mlp._EPILOGUES["none"],
                                                  case.hidden, None, 256, True),
         "combine": lambda: mlp.combine_tokens(y, lay, case.topk_weight),
@@ -235,11 +239,19 @@ def expert_mlp_summary(dev, steps: int = 20):
            "forward_ms_median": round(t_fwd, 4),
            "forward_tflops": round(case.flops / (t_fwd * 1e-3) / 1e12, 1),
            "launch_ms_median": {}}
+    # Interleaved rounds, so a clock that drifts during the measurement
+    # weighs on every launch alike.
+    times = {name: [] for name in parts}
     for name, fn in parts.items():
-        event_times_ms(fn, 20)
-        out["launch_ms_median"][name] = round(median(event_times_ms(fn, steps)), 4)
+        event_times_ms(fn, 10)
+    for rnd in range(4):
+        order = list(parts.items()) if rnd % 2 == 0 else list(parts.items())[::-1]
+        for name, fn in order:
+            times[name] += event_times_ms(fn, max(steps // 4, 5))
+    for name in parts:
+        out["launch_ms_median"][name] = round(median(times[name]), 4)
     lm = out["launch_ms_median"]
-    out["up_gemm_tflops"] = round(up_flops / (lm["up_gemm_swiglu"] * 1e-3) / 1e12, 1)
+    out["up_gemm_tflops"] = round(up_flops / (lm["up_gemm_gathered_swiglu"] * 1e-3) / 1e12, 1)
     out["down_gemm_tflops"] = round(down_flops / (lm["down_gemm"] * 1e-3) / 1e12, 1)
     del case, w1, lay, xp, h, y
     torch.cuda.empty_cache()

@@ -30,6 +30,9 @@
  *                                     csrc/kernels/layout.cu:10-121)
  *   mgg_gather_rows                -> grouped_tokens = valid_tokens[perm]
  *                                     (src/train_moe_baseline.py:224)
+ *   mgg_grouped_gemm_gathered      -> that gather and the expert MLP's first
+ *                                     GEMM in one launch
+ *                                     (src/train_moe_baseline.py:224, :239-241)
  *   mgg_grouped_gemm_fp8           -> no counterpart: the reference rejects
  *                                     fp8 (src/triton_grouped_gemm.py:357-358);
  *                                     the fp8 config of the build's baseline
@@ -195,6 +198,25 @@ int mgg_grouped_gemm_ex(int dtype, int epilogue, const void* a, const void* b, v
                         int block_m, int block_n, int num_workers, int use_atomic_queue,
                         int32_t* work_counter, int report_block_m, int report_block_n,
                         void* stream);
+
+/*
+ * mgg_grouped_gemm_ex with A's rows gathered: row r of A (r < m_size, in the
+ * expert-grouped order of expert_offsets) is row a_rows[r] of `a`, a
+ * [a_src_rows, k_size] matrix with row stride lda.  a_rows is int32 on the
+ * device; only the rows of the experts' ranges are read, and an index outside
+ * [0, a_src_rows) reads a row of zeros.  Results are bitwise those of
+ * mgg_grouped_gemm_ex on the gathered matrix (same tiles, same schedule).
+ * Covers 16-bit operands with N-major B, block_m == block_n == 256 and the
+ * device-derived queue (at most 2048 experts); every epilogue.  The
+ * work_counter is not offered (no caller-visible queue).  (Introduced with ABI
+ * version 6.)
+ */
+int mgg_grouped_gemm_gathered(int dtype, int epilogue, const void* a, const int32_t* a_rows,
+                              int64_t a_src_rows, const void* b, void* c,
+                              const int32_t* expert_offsets, int64_t m_size, int64_t k_size,
+                              int64_t n_size, int64_t num_experts, int64_t lda, int64_t ldb_e,
+                              int64_t ldb_k, int64_t ldc, int num_workers, int use_atomic_queue,
+                              void* stream);
 
 /*
  * fp8 grouped GEMM with per-token and per-channel scales:

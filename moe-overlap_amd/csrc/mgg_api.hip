@@ -220,7 +220,7 @@ using mgg::set_error;
 
 extern "C" {
 
-int mgg_abi_version(void) { return 5; }
+int mgg_abi_version(void) { return 6; }
 
 const char* mgg_last_error(void) { return mgg::g_last_error.c_str(); }
 
@@ -333,7 +333,8 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
                       const int32_t* work_tile_m, const int32_t* work_tile_n, int64_t num_work,
                       const float* a_scale, const float* b_scale, int block_m, int block_n,
                       int num_workers, int use_atomic_queue, int32_t* work_counter,
-                      int report_block_m, int report_block_n, hipStream_t st) {
+                      int report_block_m, int report_block_n, hipStream_t st,
+                      const int32_t* a_rows = nullptr, int64_t a_src_rows = 0) {
   const bool fp8 = dtype == MGG_DTYPE_FP8_E4M3;
   const int base = dtype & ~MGG_B_KMAJOR;
   const bool kmajor = (dtype & MGG_B_KMAJOR) != 0;  // 16-bit B stored [E, N, K]
@@ -393,6 +394,16 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   const int64_t b_span = b_rows_k ? ((int64_t)block_n * ldb_k + k_size) : (k_size + 8) * ldb_k;
   if ((int64_t)block_m * lda * es + k_size * es >= lim || b_span * es >= lim)
     return set_error(MGG_ERR_UNSUPPORTED, "row strides too large for 32-bit tile offsets");
+  // Gathered A: the A-block tile (256x256, 16-bit A, N-major B) with the
+  // device-derived queue; offsets into the source matrix are 32-bit.
+  if (a_rows != nullptr) {
+    if (fp8 || kmajor || block_m != 256 || block_n != 256 || num_work >= 0)
+      return set_error(MGG_ERR_UNSUPPORTED,
+                       "gathered A needs 16-bit N-major B, 256x256 tiles and the device-derived queue");
+    if (a_src_rows < 0) return set_error(MGG_ERR_INVALID, "a_src_rows must be >= 0");
+    if (a_src_rows * lda * es + k_size * es >= lim)
+      return set_error(MGG_ERR_UNSUPPORTED, "gathered A source too large for 32-bit offsets");
+  }
 
   int workers = num_workers;
   if (workers <= 0) {
@@ -445,6 +456,8 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   p.report_bm = report_block_m;
   p.report_bn = report_block_n;
   p.clock_probe = clock_probe();
+  p.a_rows = a_rows;
+  p.a_src_rows = a_rows != nullptr ? a_src_rows : 0;
   if (p.atomic) {
     int rc = counter_for(st, &p.counter);
     if (rc != MGG_OK) return rc;
@@ -494,6 +507,23 @@ int mgg_grouped_gemm_ex(int dtype, int epilogue, const void* a, const void* b, v
                                 work_tile_n, num_work, nullptr, nullptr, block_m, block_n,
                                 num_workers, use_atomic_queue, work_counter, report_block_m,
                                 report_block_n, static_cast<hipStream_t>(stream));
+}
+
+int mgg_grouped_gemm_gathered(int dtype, int epilogue, const void* a, const int32_t* a_rows,
+                              int64_t a_src_rows, const void* b, void* c,
+                              const int32_t* expert_offsets, int64_t m_size, int64_t k_size,
+                              int64_t n_size, int64_t num_experts, int64_t lda, int64_t ldb_e,
+                              int64_t ldb_k, int64_t ldc, int num_workers, int use_atomic_queue,
+                              void* stream) {
+  mgg::clear_error();
+  if (a_rows == nullptr && m_size > 0 && n_size > 0 && num_experts > 0 && k_size > 0)
+    return set_error(MGG_ERR_INVALID, "null a_rows");
+  if (dtype == MGG_DTYPE_FP8_E4M3)
+    return set_error(MGG_ERR_UNSUPPORTED, "gathered A takes 16-bit operands");
+  return mgg::grouped_gemm_impl(dtype, epilogue, a, b, c, expert_offsets, m_size, k_size, n_size,
+                                num_experts, lda, ldb_e, ldb_k, ldc, nullptr, nullptr, nullptr, -1,
+                                nullptr, nullptr, 256, 256, num_workers, use_atomic_queue, nullptr,
+                                256, 256, static_cast<hipStream_t>(stream), a_rows, a_src_rows);
 }
 
 int mgg_grouped_gemm_fp8(const void* a, const void* b, void* c, const int32_t* expert_offsets,

@@ -575,9 +575,16 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   auto b_krow = [&](int t) { return (wave * kBPerWave + t) * kBRowsPerDma + lane / kBChunks; };
   // K-major B: row n of the tile and the K position of the chunk.
   auto b_kpos = [&](int t) { return kChunkElems * ((lane % kBChunks) ^ a_swz(b_krow(t))); };
-  uint32_t a_voff[kAPerWave];  // per-lane source offsets (bytes, stage 0), the same for every tile
+  // Per-lane source offsets (bytes, stage 0): the same for every tile, or
+  // with gathered A (A-block tile) per tile from the rows' indices.
+  uint32_t a_voff[kAPerWave];
 #pragma unroll
   for (int t = 0; t < kAPerWave; ++t) a_voff[t] = (uint32_t)((a_row(t) * p.lda + a_kpos(t)) * kE);
+  // EPI: the epilogue (low two bits), plus kEpiGather for gathered A.
+  constexpr int kEpi = EPI & 3;
+  constexpr bool gathered = (EPI & kEpiGather) != 0;
+  static_assert(!gathered || kABlk, "gathered A is built on the A-block tile");
+  int32_t a_tok[kAPerWave];  // gathered A: source row of each of this lane's A rows, or -1
   const uint32_t b_row_bytes = (uint32_t)(p.ldb_k * kE);
   const uint32_t lds_a0 = lds_addr(lds);
   const uint32_t lds_b0 = lds_a0 + kASlots * kASlot;
@@ -610,8 +617,13 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     }
     k_size = klen;
     nk = (klen + kBK - 1) / kBK;
-    const int64_t a_end = r0 < r_end ? ((r_end - 1 - r0) * p.lda + klen) * kE : 0;
-    a_rsrc = make_rsrc4(a_bytes + (r0 * p.lda + kb) * kE, a_end);
+    if constexpr (gathered) {  // rows anywhere in the source matrix; per-lane offsets from set_a_rows
+      const int64_t a_end = p.a_src_rows > 0 ? ((p.a_src_rows - 1) * p.lda + klen) * kE : 0;
+      a_rsrc = make_rsrc4(a_bytes + (int64_t)kb * kE, a_end);
+    } else {
+      const int64_t a_end = r0 < r_end ? ((r_end - 1 - r0) * p.lda + klen) * kE : 0;
+      a_rsrc = make_rsrc4(a_bytes + (r0 * p.lda + kb) * kE, a_end);
+    }
     if constexpr (T::kBKMajor) {
       const int64_t b_end = c.n0 < p.n ? ((p.n - 1 - c.n0) * p.ldb_k + klen) * kE : 0;
       b_rsrc = make_rsrc4(b_bytes + ((int64_t)c.e * p.ldb_e + c.n0 * p.ldb_k + kb) * kE, b_end);
@@ -630,6 +642,23 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
         b_voff[t] = (uint32_t)((k * p.ldb_k + col) * 2);
       }
     }
+  };
+
+  // Gathered A: load the source row index of each of this lane's A rows of
+  // tile c (ordinary loads, issued ahead of their use), then turn them into
+  // the lane's DMA offsets.  Rows past the tile's valid rows, and indices
+  // outside the source matrix, get offsets past the descriptor (zeros).
+  auto load_rows = [&](const Coords& c) {
+#pragma unroll
+    for (int t = 0; t < kAPerWave; ++t)
+      a_tok[t] = a_row(t) < c.rows_valid ? p.a_rows[c.row_base + a_row(t)] : -1;
+  };
+  auto set_a_rows = [&]() {
+#pragma unroll
+    for (int t = 0; t < kAPerWave; ++t)
+      a_voff[t] = a_tok[t] >= 0 && a_tok[t] < p.a_src_rows
+                      ? (uint32_t)(((int64_t)a_tok[t] * p.lda + a_kpos(t)) * kE)
+                      : kOutOfRange;
   };
 
   // Issues DMAs [d0, d1) of this wave's kDmaPerStage DMAs of stage s (the
@@ -1032,8 +1061,8 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // epilogue B's columns come interleaved in groups of 64 (32 gate columns,
   // then the 32 up columns of the same outputs), so a wave's 32-column blocks
   // 2i and 2i+1 are gate and up of the same 32 outputs and C has N/2 columns.
-  static_assert(EPI != kEpiSwiglu || kNB % 2 == 0, "SwiGLU needs pairs of 32-column blocks per wave");
-  static_assert(EPI == kEpiNone || !T::kScaled, "fused epilogues are for unscaled types");
+  static_assert(kEpi != kEpiSwiglu || kNB % 2 == 0, "SwiGLU needs pairs of 32-column blocks per wave");
+  static_assert(kEpi == kEpiNone || !T::kScaled, "fused epilogues are for unscaled types");
   // Stores: a lane holds 4 consecutive columns of each 8-column group g; the
   // lanes l and l+32 of one row swap halves of groups (2p, 2p+1) with
   // v_permlane32_swap so that each lane stores 8 consecutive columns (16 bytes)
@@ -1077,7 +1106,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // left in L2 it would evict A and B lines that other tiles still read
   // (measured: skewed routing and the atomic schedule 4-5.5% faster, fp8
   // 3.5-5%).
-  constexpr int kOutCols = EPI == kEpiSwiglu ? BN / kWN / 2 : BN / kWN;  // per wave and row
+  constexpr int kOutCols = kEpi == kEpiSwiglu ? BN / kWN / 2 : BN / kWN;  // per wave and row
   constexpr int kLineChunks = kOutCols * 2 / 16;  // 16-byte chunks of a wave's row segment
   constexpr bool kLineStores =
       (kLineChunks == 4 || kLineChunks == 8) &&
@@ -1130,7 +1159,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       const bool row_ok = m < c.rows_valid && grow >= 0 && grow <= last_row;
       uint16_t* crow = p.c + grow * p.ldc;
       const int ol = kLineStores ? opaque_lane() : lane;
-      if constexpr (EPI == kEpiSwiglu) {
+      if constexpr (kEpi == kEpiSwiglu) {
 #pragma unroll
         for (int ip = 0; ip < kNB / 2; ++ip) {
           const int64_t f0 = (c.n0 + wn * (BN / kWN) + 64 * ip) / 2;
@@ -1163,7 +1192,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
                 const int g = 2 * pp + h;
                 float v = acc[i][j][4 * g + q];
                 if constexpr (T::kScaled) v *= row_scale * sc[BM + cb + 8 * g + 4 * half + q];
-                y[h][q] = EPI == kEpiGelu ? gelu_erf(v) : v;
+                y[h][q] = kEpi == kEpiGelu ? gelu_erf(v) : v;
               }
             if constexpr (kLineStores)
               line_put(ol & 31, 4 * i + 2 * pp + (ol >> 5), pack_pair(y[0], y[1]));
@@ -1298,6 +1327,10 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   if ((uint32_t)w >= (uint32_t)W) return;
   set_sources(cur, scale_buf);
   if constexpr (kABlk) {
+    if constexpr (gathered) {
+      load_rows(cur);
+      set_a_rows();
+    }
     prologue_ab(false);
   } else {
 #pragma unroll
@@ -1319,18 +1352,31 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     const bool more = (uint32_t)next < (uint32_t)W;
     // The next tile's first stage goes out before this tile's stores and its
     // other prologue stages after them, so each later wait only ever counts
-    // DMAs issued after the stage it waits for.
+    // DMAs issued after the stage it waits for.  Gathered A: the next tile's
+    // row indices are loaded first and its B stage 0 goes out, the stores
+    // cover the indices' latency, then A block 0 follows (the first wait
+    // still finds B stages 1 .. kLB-1 issued after both).
     issued = -1;
     if (more) {
       set_sources(nxt, scale_buf ^ 1);
-      if constexpr (kABlk)
-        prologue_ab(true);
-      else if (nk > 0)
+      if constexpr (kABlk) {
+        if constexpr (gathered) {
+          load_rows(nxt);
+          issue_bstage(0, 0, kBPerWave);
+        } else {
+          prologue_ab(true);
+        }
+      } else if (nk > 0) {
         issue_stage(issued = 0);
+      }
     }
     if (store_cur) epilogue(cur);
     if (!more) break;
     if constexpr (kABlk) {
+      if constexpr (gathered) {
+        set_a_rows();
+        issue_ablock(0, 0, kAPerWave);
+      }
       for (int st = 1; st < kLB; ++st) issue_bstage(st, 0, kBPerWave);
     } else {
 #pragma unroll
@@ -1402,7 +1448,7 @@ grouped_gemm_kernel(GemmParams p) {
                               rep_tiles, &w_report);
   }
   if (W == 0) {
-    zero_fill(p, EPI == kEpiSwiglu ? p.n / 2 : p.n);
+    zero_fill(p, (EPI & 3) == kEpiSwiglu ? p.n / 2 : p.n);
     return;
   }
 
@@ -1485,9 +1531,31 @@ int launch_fp8(int block_m, int block_n, const GemmParams& p, int workers, hipSt
   return set_error(MGG_ERR_UNSUPPORTED, "fp8 tiles are 256x256, 256x128, 192x128 and 128x128");
 }
 
+// Gathered A: the 256x256 A-block tile only (the host checks the shape).
+template <class T, int EPI>
+int launch_gathered(const GemmParams& p, int workers, hipStream_t stream) {
+  hipLaunchKernelGGL((grouped_gemm_kernel<256, 256, MGG_SBK256, MGG_NS256, MGG_NW256, T, EPI | kEpiGather>),
+                     dim3(workers), dim3(MGG_NW256 * 64), 0, stream, p);
+  return MGG_OK;
+}
+
 template <class T>
 int launch_epi(int epilogue, int block_m, int block_n, const GemmParams& p, int workers,
                hipStream_t stream) {
+  if constexpr (!T::kBKMajor && !T::kScaled) {
+    if (p.a_rows != nullptr) {
+      if (block_m != 256 || block_n != 256)
+        return set_error(MGG_ERR_UNSUPPORTED, "gathered A needs 256x256 tiles");
+      switch (epilogue) {
+        case kEpiNone: return launch_gathered<T, kEpiNone>(p, workers, stream);
+        case kEpiGelu: return launch_gathered<T, kEpiGelu>(p, workers, stream);
+        case kEpiSwiglu: return launch_gathered<T, kEpiSwiglu>(p, workers, stream);
+        default: return set_error(MGG_ERR_INVALID, "unknown epilogue");
+      }
+    }
+  } else {
+    if (p.a_rows != nullptr) return set_error(MGG_ERR_UNSUPPORTED, "gathered A needs N-major 16-bit B");
+  }
   switch (epilogue) {
     case kEpiNone: return launch_typed<T, kEpiNone>(block_m, block_n, p, workers, stream);
     case kEpiGelu: return launch_typed<T, kEpiGelu>(block_m, block_n, p, workers, stream);

@@ -26,6 +26,9 @@ constexpr int kMaxLayoutExperts = 8192;
 constexpr int kEpiNone = 0;
 constexpr int kEpiGelu = 1;
 constexpr int kEpiSwiglu = 2;
+// OR'd into a kernel's epilogue template argument (never an MGG_EPI_* value):
+// the instance that reads A's rows through GemmParams::a_rows.
+constexpr int kEpiGather = 4;
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -75,6 +78,11 @@ struct GemmParams {
   float* split_partials;
   unsigned long long* split_flags;
   int32_t split_slots;
+  // Gathered A (null normally; A-block tiles with the device-derived queue
+  // only): row r of A is row a_rows[r] of the [a_src_rows, K] matrix at `a`.
+  // Indices outside [0, a_src_rows) read zeros.
+  const int32_t* a_rows;
+  int64_t a_src_rows;
 };
 
 // The clock probe buffer set by mgg_debug_set_clock_probe (null: off).

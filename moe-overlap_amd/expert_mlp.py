@@ -185,12 +185,44 @@ def expert_mlp_forward(
     if w2.shape[0] != E or w2.shape[1] != F or w2.shape[2] != x.shape[1]:
         raise ValueError("w2 must be [E, F, H] matching w1 and x")
     layout = dispatch_layout(topk_idx, E)
-    xp = permute_tokens(x, layout)
-    h = _grouped_gemm_ex(xp, w1, layout.offsets, _EPILOGUES[activation], F, num_sms, block,
-                         use_atomic_queue)
+    if _gathered_ok(x, w1, block):
+        # The gather of train:224 runs inside the up GEMM: its A rows are read
+        # from x through layout.token_index (bitwise the same result).
+        h = _grouped_gemm_gathered(x, layout, w1, _EPILOGUES[activation], F, num_sms,
+                                   use_atomic_queue)
+    else:
+        xp = permute_tokens(x, layout)
+        h = _grouped_gemm_ex(xp, w1, layout.offsets, _EPILOGUES[activation], F, num_sms, block,
+                             use_atomic_queue)
     y = _grouped_gemm_ex(h, w2, layout.offsets, nat.MGG_EPI_NONE, x.shape[1], num_sms, block,
                          use_atomic_queue)
     return combine_tokens(y, layout, topk_weight)
+
+
+def _gathered_ok(x, w1, block):
+    """Whether the up GEMM can read its A rows from x in place: the 256x256
+    tile with N-major weights, the device-derived queue, 16-byte aligned rows
+    and 32-bit offsets into x."""
+    return (block == 256 and w1.shape[0] <= nat.MAX_DEVICE_QUEUE_EXPERTS
+            and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
+            and w1.stride(2) == 1 and w1.stride(1) % 8 == 0 and w1.stride(0) % 8 == 0
+            and w1.data_ptr() % 16 == 0 and x.shape[1] % 8 == 0 and w1.shape[2] % 8 == 0
+            and (x.shape[0] * x.stride(0) + x.shape[1]) * 2 < (1 << 31) - 4096)
+
+
+def _grouped_gemm_gathered(x, layout, w1, epilogue, out_cols, num_sms, use_atomic_queue):
+    """C [T*k, out_cols] = epilogue(x[token_index] @ w1[e]) over the expert row
+    ranges of the layout, in one launch (rows past offsets[E] unwritten)."""
+    T, H = x.shape
+    E, _, N = w1.shape
+    M = layout.max_rows
+    c = torch.empty(M, out_cols, dtype=x.dtype, device=x.device)
+    with torch.cuda.device(x.device):
+        nat.check(nat.lib().mgg_grouped_gemm_gathered(
+            _DTYPES[x.dtype], epilogue, _p(x), _p(layout.token_index), T, _p(w1), _p(c),
+            _p(layout.offsets), M, H, N, E, x.stride(0), w1.stride(0), w1.stride(1), c.stride(0),
+            int(num_sms) if num_sms else 0, 1 if use_atomic_queue else 0, _stream_ptr(x.device)))
+    return c
 
 
 def _grouped_gemm_ex(a, b, offsets, epilogue, out_cols, num_sms, block, use_atomic_queue):

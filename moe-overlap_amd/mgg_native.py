@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime this library must share)
 
 LIB_PATH = Path(__file__).resolve().parent / "libmgg.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 MGG_OK = 0
 MGG_ERR_INVALID = 1
@@ -60,6 +60,12 @@ _SIGNATURES = {
         _c_ptr, _c_ptr, _c_ptr, _c_i64,  # queue, num_work
         _c_i32, _c_i32, _c_i32, _c_i32,  # block_m, block_n, num_workers, atomic
         _c_ptr, _c_i32, _c_i32, _c_ptr,  # work_counter, report_block_m/n, stream
+    ],
+    "mgg_grouped_gemm_gathered": [
+        _c_i32, _c_i32, _c_ptr, _c_ptr, _c_i64,  # dtype, epilogue, a, a_rows, a_src_rows
+        _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64,  # b, c, offsets, M, K, N
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,  # E, lda, ldb_e, ldb_k, ldc
+        _c_i32, _c_i32, _c_ptr,  # num_workers, atomic, stream
     ],
     "mgg_grouped_gemm_ex": [
         _c_i32, _c_i32, _c_ptr, _c_ptr, _c_ptr,  # dtype, epilogue, a, b, c

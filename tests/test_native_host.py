@@ -124,6 +124,31 @@ def test_gemm_validation_rejects_before_launch(over, code, text):
     assert text in nat.lib().mgg_last_error()
 
 
+def gathered_call(**over):
+    args = dict(dtype=nat.MGG_DTYPE_BF16, epi=nat.MGG_EPI_NONE, a=FAKE, rows=FAKE, src=64, b=FAKE,
+                c=FAKE, off=FAKE, m=64, k=64, n=256, e=1, lda=64, ldb_e=64 * 256, ldb_k=256,
+                ldc=256, workers=4, atomic=0, stream=None)
+    args.update(over)
+    return nat.lib().mgg_grouped_gemm_gathered(*args.values())
+
+
+@pytest.mark.parametrize("over, code, text", [
+    (dict(rows=None), nat.MGG_ERR_INVALID, b"a_rows"),
+    (dict(dtype=nat.MGG_DTYPE_FP8_E4M3), nat.MGG_ERR_UNSUPPORTED, b"16-bit"),
+    (dict(dtype=nat.MGG_DTYPE_BF16 | nat.MGG_B_KMAJOR, ldb_k=64), nat.MGG_ERR_UNSUPPORTED,
+     b"gathered A needs"),
+    (dict(src=-1), nat.MGG_ERR_INVALID, b"a_src_rows"),
+    (dict(src=1 << 24), nat.MGG_ERR_UNSUPPORTED, b"32-bit"),
+    (dict(lda=32), nat.MGG_ERR_INVALID, b"leading"),
+    (dict(e=4096), nat.MGG_ERR_UNSUPPORTED, b"2048 experts"),
+])
+def test_gathered_validation_rejects_before_launch(over, code, text):
+    """The gathered up GEMM covers the A-block tile only (16-bit, N-major B,
+    256x256, device-derived queue) and 32-bit offsets into the source rows."""
+    assert gathered_call(**over) == code
+    assert text in nat.lib().mgg_last_error()
+
+
 def test_gemm_empty_output_is_a_no_op():
     assert gemm_call(m=0) == nat.MGG_OK
     assert gemm_call(n=0) == nat.MGG_OK
