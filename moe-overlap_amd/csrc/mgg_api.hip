@@ -358,8 +358,13 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   if (m_size < 0 || k_size < 0 || n_size < 0 || num_experts < 0)
     return set_error(MGG_ERR_INVALID, "sizes must be >= 0");
   if (m_size == 0 || n_size == 0) return MGG_OK;  // C has no elements
-  if (k_size % 8 != 0 || n_size % 8 != 0)
-    return set_error(MGG_ERR_UNSUPPORTED, "K and N must be multiples of 8");
+  if (n_size % 8 != 0) return set_error(MGG_ERR_UNSUPPORTED, "K and N must be multiples of 8");
+  // K not a multiple of 8 (16-bit N-major B only): A is read to the next
+  // multiple of 8 (those columns meet B rows that read as zeros), B's rows
+  // stop at K.
+  if (k_size % 8 != 0 && (fp8 || b_rows_k))
+    return set_error(MGG_ERR_UNSUPPORTED, "K and N must be multiples of 8 (K-major B, fp8)");
+  const int64_t k_a = (k_size + 7) / 8 * 8;
   // K == 0: nothing is read (every DMA is past its descriptor, so the tiles
   // hold zeros); A's and B's strides are then unused.
   if (k_size == 0) {
@@ -376,7 +381,7 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   // B, N rows of K values).
   if (report_block_m <= 0) report_block_m = block_m;
   if (report_block_n <= 0) report_block_n = block_n;
-  if (lda < k_size || ldb_k < (b_rows_k ? k_size : n_size) || ldc < c_cols || ldb_e < 0)
+  if (lda < k_a || ldb_k < (b_rows_k ? k_size : n_size) || ldc < c_cols || ldb_e < 0)
     return set_error(MGG_ERR_INVALID, "leading dimensions smaller than the matrix extents");
   if (lda % 8 != 0 || ldb_k % 8 != 0 || ldb_e % 8 != 0 || ldc % 8 != 0)
     return set_error(MGG_ERR_UNSUPPORTED, "strides must be multiples of 8 elements");
@@ -392,7 +397,7 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   const int64_t lim = ((int64_t)1 << 31) - 4096;
   const int64_t es = fp8 ? 1 : 2;
   const int64_t b_span = b_rows_k ? ((int64_t)block_n * ldb_k + k_size) : (k_size + 8) * ldb_k;
-  if ((int64_t)block_m * lda * es + k_size * es >= lim || b_span * es >= lim)
+  if ((int64_t)block_m * lda * es + k_a * es >= lim || b_span * es >= lim)
     return set_error(MGG_ERR_UNSUPPORTED, "row strides too large for 32-bit tile offsets");
   // Gathered A: the A-block tile (256x256, 16-bit A, N-major B) with the
   // device-derived queue; offsets into the source matrix are 32-bit.
@@ -401,7 +406,7 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
       return set_error(MGG_ERR_UNSUPPORTED,
                        "gathered A needs 16-bit N-major B, 256x256 tiles and the device-derived queue");
     if (a_src_rows < 0) return set_error(MGG_ERR_INVALID, "a_src_rows must be >= 0");
-    if (a_src_rows * lda * es + k_size * es >= lim)
+    if (a_src_rows * lda * es + k_a * es >= lim)
       return set_error(MGG_ERR_UNSUPPORTED, "gathered A source too large for 32-bit offsets");
   }
 
@@ -441,7 +446,8 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   p.q_tile_m = num_work >= 0 ? work_tile_m : nullptr;
   p.q_tile_n = num_work >= 0 ? work_tile_n : nullptr;
   p.m = m_size;
-  p.k = k_size;
+  p.k = k_a;
+  p.k_b = k_size;
   p.n = n_size;
   p.lda = lda;
   p.ldb_e = ldb_e;

@@ -40,9 +40,11 @@ Differences, all in arguments that do not change results:
   in the last bits from the striped schedule's (both within the tolerance of
   the fp32 product; each repeats itself bitwise).  Graph-captured launches
   and prebuilt queues take whole tiles.
-* Operands whose inner stride is not 1, whose rows are not 16-byte aligned, or
-  with K or N not a multiple of 8, are copied (and zero-padded) on the device
-  first.  K == 0 gives zeros, as there.
+* Operands whose inner stride is not 1 or whose rows are not 16-byte aligned
+  are copied on the device first.  K not a multiple of 8: A is copied with
+  zero columns to the next multiple of 8 and B is read in place (the kernel
+  stops B's rows at K; a K-major B view is copied).  N not a multiple of 8: B
+  is copied zero-padded and C sliced.  K == 0 gives zeros, as there.
 """
 from __future__ import annotations
 
@@ -351,7 +353,10 @@ def persistent_grouped_gemm(
         raise ValueError("num_sms must be positive.")
     counter_dev = _counter_arg(work_counter, use_atomic_queue, device)
 
-    # K or N not a multiple of 8: zero-pad on the device (zeros add nothing).
+    # K not a multiple of 8: A is zero-padded on the device to the next
+    # multiple of 8 and B is read as it lies (the kernel stops B's rows at K,
+    # so the padding columns meet zeros).  N not a multiple of 8: B is
+    # zero-padded and C sliced.
     k_pad = (k_size + 7) // 8 * 8
     n_pad = (n_size + 7) // 8 * 8
     a_op, b_op = a_cat, b_expert
@@ -359,7 +364,6 @@ def persistent_grouped_gemm(
     b_kmajor = k_pad == k_size and n_pad == n_size and _kmajor_layout(b_expert)
     if k_pad != k_size:
         a_op = torch.nn.functional.pad(a_op, (0, k_pad - k_size))
-        b_op = torch.nn.functional.pad(b_op, (0, 0, 0, k_pad - k_size))
     if n_pad != n_size:
         b_op = torch.nn.functional.pad(b_op, (0, n_pad - n_size))
     if k_pad > 0:
@@ -374,8 +378,8 @@ def persistent_grouped_gemm(
         ldb_k = b_op.stride(2)
         ldb_e = b_op.stride(0) if num_experts > 1 else n_pad * ldb_k
     else:
-        ldb_k = b_op.stride(1) if k_pad > 1 else n_pad
-        ldb_e = b_op.stride(0) if num_experts > 1 else k_pad * ldb_k
+        ldb_k = b_op.stride(1) if k_size > 1 else n_pad
+        ldb_e = b_op.stride(0) if num_experts > 1 else k_size * ldb_k
     dtype_code = _DTYPE_CODES[a_cat.dtype] | (_nat.MGG_B_KMAJOR if b_kmajor else 0)
     c_op = torch.empty((m_total, n_pad), device=device, dtype=a_cat.dtype)
 
@@ -383,7 +387,7 @@ def persistent_grouped_gemm(
     off32 = _offsets_i32(expert_offsets)
     args = (
         dtype_code, _ptr(a_op), _ptr(b_op), _ptr(c_op),
-        _ptr(off32), m_total, k_pad, n_pad,
+        _ptr(off32), m_total, k_size, n_pad,
         num_experts, lda, ldb_e, ldb_k, c_op.stride(0),
         _ptr(we), _ptr(wm), _ptr(wn), num_work,
         kbm, kbn, int(num_sms), 1 if use_atomic_queue else 0,

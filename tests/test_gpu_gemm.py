@@ -289,6 +289,36 @@ def test_odd_shapes_are_padded(cuda_device):
     assert_parity(c, a, b, offs, 50)
 
 
+K_TAILS = [1, 3, 7, 13, 50, 257, 1001, 2044]
+
+
+@pytest.mark.parametrize("k", K_TAILS)
+@pytest.mark.parametrize("tile", [(256, 256), (128, 128), (64, 64)])
+def test_k_tail_reads_b_in_place(cuda_device, k, tile):
+    """K not a multiple of 8: A is zero-padded, B (N-major, allocated exactly
+    [E, K, N], the last expert non-empty) is read as it lies with its rows
+    stopped at K.  Bitwise equal to the fully zero-padded problem, for both
+    schedules (the atomic one splitting its last round where K allows)."""
+    log(f"k tail k={k} tile={tile}")
+    a, b, offs = make_inputs([70, 0, 300, 1, 260], k, 264, torch.bfloat16, cuda_device, seed=k)
+    kp = (k + 7) // 8 * 8
+    a_pad = torch.nn.functional.pad(a, (0, kp - k))
+    b_pad = torch.nn.functional.pad(b, (0, 0, 0, kp - k))
+    for atomic in (False, True):
+        c = gg.persistent_grouped_gemm(a, b, offs, kernel_tile=tile, use_atomic_queue=atomic)
+        c_pad = gg.persistent_grouped_gemm(a_pad, b_pad, offs, kernel_tile=tile,
+                                           use_atomic_queue=atomic)
+        torch.cuda.synchronize()
+        assert torch.equal(c, c_pad), atomic
+    # Against the fp64 oracle: one bf16 rounding of the output (relative
+    # 2^-8; with K = 1 the outputs are products of two N(0, 1) values, so an
+    # absolute bound alone would not fit) plus the fp32 accumulation's share.
+    rows = covered_rows(offs)
+    want = oracle_out(a, b, offs)[rows]
+    got = c.float().cpu().numpy()[rows]
+    assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + 1e-3 * math.sqrt(k))
+
+
 def test_strided_operands(cuda_device):
     a_wide, b, offs = make_inputs([33, 70], 128, 64, torch.bfloat16, cuda_device)
     big = torch.randn(103, 256, device=cuda_device).to(torch.bfloat16)

@@ -100,7 +100,11 @@ def gemm_call(**over):
     (dict(dtype=7), nat.MGG_ERR_UNSUPPORTED, b"dtype"),
     (dict(bm=96), nat.MGG_ERR_UNSUPPORTED, b"block_m"),
     (dict(bn=512), nat.MGG_ERR_UNSUPPORTED, b"block_m"),
-    (dict(k=60, lda=64), nat.MGG_ERR_UNSUPPORTED, b"multiples of 8"),
+    # K need not be a multiple of 8 for N-major 16-bit B (A is read to the next
+    # multiple, B's rows stop at K), but must be for K-major B.
+    (dict(dtype=nat.MGG_DTYPE_BF16 | nat.MGG_B_KMAJOR, k=60, lda=64, ldb_k=64, ldb_e=64 * 64),
+     nat.MGG_ERR_UNSUPPORTED, b"multiples of 8"),
+    (dict(k=60, lda=56), nat.MGG_ERR_INVALID, b"leading"),
     (dict(n=60), nat.MGG_ERR_UNSUPPORTED, b"multiples of 8"),
     (dict(lda=32), nat.MGG_ERR_INVALID, b"leading"),
     (dict(ldb_k=72, ldb_e=60), nat.MGG_ERR_UNSUPPORTED, b"strides"),
