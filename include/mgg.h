@@ -163,10 +163,15 @@ int mgg_build_work_queue_host(const int64_t* expert_offsets, int64_t num_experts
  * If the queue is empty, C is zero-filled; with K == 0 the covered rows are
  * zeros (A and B and their strides are not read).  Rows of C not covered by
  * any expert range are left unwritten.  Supported: dtype BF16/FP16,
- * block_m, block_n in {64, 128, 256}, K % 8 == 0, N % 8 == 0, strides
- * multiples of 8 elements, 16-byte aligned base pointers, E <= 2048 when the
- * queue is derived on the device.
- * (ABI version 4 added report_block_m, report_block_n.)
+ * block_m, block_n in {64, 128, 256}, N % 8 == 0, strides multiples of 8
+ * elements, 16-byte aligned base pointers, E <= 2048 when the queue is
+ * derived on the device.  K % 8 == 0 for K-major B; with N-major B any K:
+ * B's rows at and past K are never read (they count as zeros), while A is
+ * read up to the next multiple of 8, so lda must cover it and A's elements
+ * in those columns must be finite (they are multiplied by zeros; the drop-in
+ * makes them zeros).
+ * (ABI version 4 added report_block_m, report_block_n; version 6 any K for
+ * N-major B.)
  */
 int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
                      const int32_t* expert_offsets, int64_t m_size, int64_t k_size, int64_t n_size,
