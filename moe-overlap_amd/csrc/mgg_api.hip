@@ -446,8 +446,7 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   p.q_tile_m = num_work >= 0 ? work_tile_m : nullptr;
   p.q_tile_n = num_work >= 0 ? work_tile_n : nullptr;
   p.m = m_size;
-  p.k = k_a;
-  p.k_b = k_size;
+  p.k = k_size;
   p.n = n_size;
   p.lda = lda;
   p.ldb_e = ldb_e;

@@ -500,7 +500,6 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // K extent of the tile being issued (set by set_sources): all of K, or one
   // half of it for a split tile.
   int k_size = (int)K;
-  int kb_size = (int)p.k_b;  // N-major B: rows of the issued item's K range that B holds
   int nk = (int)((K + kBK - 1) / kBK);
 
   const int64_t last_row = p.m - 1;
@@ -617,13 +616,17 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       klen = ke - kb;
     }
     k_size = klen;
-    kb_size = klen;
     nk = (klen + kBK - 1) / kBK;
+    // A's rows are read to the next multiple of 8 columns past the item's K
+    // range: with K not a multiple of 8, the 16-byte chunk that holds K-1
+    // also holds columns up to that multiple (they meet B rows past K, which
+    // read as zeros).
+    const int64_t klen_a = (klen + 7) & ~7;
     if constexpr (gathered) {  // rows anywhere in the source matrix; per-lane offsets from set_a_rows
-      const int64_t a_end = p.a_src_rows > 0 ? ((p.a_src_rows - 1) * p.lda + klen) * kE : 0;
+      const int64_t a_end = p.a_src_rows > 0 ? ((p.a_src_rows - 1) * p.lda + klen_a) * kE : 0;
       a_rsrc = make_rsrc4(a_bytes + (int64_t)kb * kE, a_end);
     } else {
-      const int64_t a_end = r0 < r_end ? ((r_end - 1 - r0) * p.lda + klen) * kE : 0;
+      const int64_t a_end = r0 < r_end ? ((r_end - 1 - r0) * p.lda + klen_a) * kE : 0;
       a_rsrc = make_rsrc4(a_bytes + (r0 * p.lda + kb) * kE, a_end);
     }
     if constexpr (T::kBKMajor) {
@@ -633,10 +636,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       for (int t = 0; t < kBPerWave; ++t)
         b_voff[t] = (uint32_t)((b_krow(t) * p.ldb_k + b_kpos(t)) * kE);
     } else {
-      // B's rows stop at k_b (K not a multiple of 8: A's columns up to the
-      // next multiple of 8 meet rows of zeros).
-      kb_size = (int)(p.k_b - kb < klen ? (p.k_b - kb > 0 ? p.k_b - kb : 0) : klen);
-      const int64_t b_end = kb_size > 0 ? ((kb_size - 1) * p.ldb_k + p.n - c.n0) * 2 : 0;
+      const int64_t b_end = ((klen - 1) * p.ldb_k + p.n - c.n0) * 2;
       b_rsrc = make_rsrc4(b_bytes + ((int64_t)c.e * p.ldb_e + c.n0 + kb * p.ldb_k) * 2, b_end);
 #pragma unroll
       for (int t = 0; t < kBPerWave; ++t) {
@@ -677,7 +677,6 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     const uint32_t la = lds_a0 + buf * kAStage + wave * kAPerWave * 1024;
     const uint32_t lb = lds_b0 + buf * kBStage + wave * kBPerWave * 1024;
     const bool full = k0 + kBK <= k_size;
-    const bool full_b = k0 + kBK <= kb_size;
 #pragma unroll
     for (int d = d0; d < d1; ++d) {
       if (d < kAPerWave) {
@@ -698,11 +697,11 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
                 k0 + b_kpos(t) < k_size ? b_voff[t] + (uint32_t)k0 * kE : kOutOfRange;
             dma16(b_rsrc, v, 0u, lb + t * 1024);
           }
-        } else if (full_b) {
+        } else if (full) {
           dma16(b_rsrc, b_voff[t], (uint32_t)k0 * b_row_bytes, lb + t * 1024);
         } else {
           const uint32_t v =
-              k0 + b_krow(t) < kb_size ? b_voff[t] + (uint32_t)k0 * b_row_bytes : kOutOfRange;
+              k0 + b_krow(t) < k_size ? b_voff[t] + (uint32_t)k0 * b_row_bytes : kOutOfRange;
           dma16(b_rsrc, v, 0u, lb + t * 1024);
         }
       }
@@ -953,14 +952,14 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   auto issue_bstage = [&](int st, int d0, int d1) {  // DMAs [d0, d1) of B stage st
     const int k0 = st * kBK;
     const uint32_t lb = lds_b0 + (st % kBSlots) * kBStage + wave * kBPerWave * 1024;
-    const bool full = k0 + kBK <= kb_size;
+    const bool full = k0 + kBK <= k_size;
 #pragma unroll
     for (int t = d0; t < d1; ++t) {
       if (full) {
         dma16(b_rsrc, b_voff[t], (uint32_t)k0 * b_row_bytes, lb + t * 1024);
       } else {
         const uint32_t v =
-            k0 + b_krow(t) < kb_size ? b_voff[t] + (uint32_t)k0 * b_row_bytes : kOutOfRange;
+            k0 + b_krow(t) < k_size ? b_voff[t] + (uint32_t)k0 * b_row_bytes : kOutOfRange;
         dma16(b_rsrc, v, 0u, lb + t * 1024);
       }
     }

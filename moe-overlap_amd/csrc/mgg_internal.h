@@ -48,8 +48,7 @@ struct GemmParams {
   unsigned long long* counter;
   int32_t* report;   // atomic mode: caller's work_counter, receives W_report + G, or null
   int64_t m;
-  int64_t k;    // K extent of A (stages), a multiple of 8
-  int64_t k_b;  // rows of N-major B, <= k: B's rows at and past k_b read as zeros
+  int64_t k;  // any K for N-major 16-bit B (A's rows are read to the next multiple of 8)
   int64_t n;
   int64_t lda;
   int64_t ldb_e;
