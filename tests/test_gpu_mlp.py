@@ -98,9 +98,10 @@ def test_gather_rows_bit_exact(cuda_device):
 
 
 @pytest.mark.parametrize("H", [256, 13])
-def test_combine_matches_oracle(cuda_device, H):
-    log(f"combine H={H}")
-    T, k, E = 257, 4, 9
+@pytest.mark.parametrize("k", [1, 4, 10])  # 10: more slots than the kernel loads together
+def test_combine_matches_oracle(cuda_device, H, k):
+    log(f"combine H={H} k={k}")
+    T, E = 257, 12
     idx, w = random_routing(T, k, E, masked_every=3)
     lay = mlp.dispatch_layout(idx.to(cuda_device), E)
     y = torch.randn(T * k, H).to(torch.bfloat16)
