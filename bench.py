@@ -152,12 +152,13 @@ def settle_clock(fn, min_ms=50.0, window=10, rel=0.02, max_s=5.0):
 
 
 def clock_pass(fn, launches=50):
-    """Average shader clock over `launches` back-to-back launches of fn: the
-    shader-clock ticks a workgroup lives (s_memtime, libmgg's clock probe,
-    eight workgroups per launch) over the per-launch time from HIP events
-    around the pass.  A workgroup lives a little less than its launch, so
-    this reads up to a few percent low.  A pass of its own, so the probe
-    stays out of the other timings."""
+    """s_memtime ticks per microsecond over `launches` back-to-back launches
+    of fn (libmgg's clock probe: the ticks eight workgroups live, over the
+    per-launch time from HIP events around the pass).  On gfx950 s_memtime
+    does not count shader clocks (an MFMA-only probe at 97.6% of peak read
+    1244), so this is only a relative reading between runs of one box, not
+    the clock; rocprofv3's GRBM_GUI_ACTIVE gives cycle counts.  A pass of
+    its own, so the probe stays out of the other timings."""
     import torch
 
     import mgg_native as nat
@@ -172,9 +173,10 @@ def clock_pass(fn, launches=50):
         nat.check(lib.mgg_debug_set_clock_probe(None))
     ticks, readers = probe.tolist()
     mhz = ticks / readers / (ms * 1e3) if readers > 0 and ms > 0 else None
-    return {"sclk_mhz": round(mhz, 1) if mhz else None, "launches": launches,
+    return {"s_memtime_ticks_per_us": round(mhz, 1) if mhz else None, "launches": launches,
             "ms_per_launch": round(ms, 5),
-            "source": "s_memtime ticks of a workgroup's lifetime / HIP-event time per launch"}
+            "source": "s_memtime ticks of a workgroup's lifetime / HIP-event time per launch "
+                      "(a relative reading: s_memtime is not the shader clock on gfx950)"}
 
 
 PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_256x256_bf16_uniform.md"
@@ -686,11 +688,6 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
             "achieved_from": "HIP events around the timed steps (GPU time per launch)",
-            # The published peak assumes the 2.4 GHz peak clock; the card sustains less under
-            # this kernel (power-limited), measured by the clock pass.
-            "frac_of_peak_at_sustained_clock": (
-                round(achieved / (PEAK_BF16_TFLOPS * r["clock"]["sclk_mhz"] / 2400.0), 4)
-                if r["clock"].get("sclk_mhz") else None),
             "traffic": recorded_traffic(args.mode, args.workload, kernel_tile),
             "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), "
                               "profiles/grouped_gemm_256x256_bf16_uniform.md",
