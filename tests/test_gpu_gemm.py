@@ -202,10 +202,11 @@ def sampled_parity(c, case, offs, stride=16):
     return err
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("name", ["uniform", "skewed"])
-def test_full_size_configs(cuda_device, name):
-    case = workloads.make_case(name, device="cpu", dtype=torch.bfloat16)
-    log(f"full-size {name}: M={case.m}")
+def test_full_size_configs(cuda_device, name, dtype):
+    case = workloads.make_case(name, device="cpu", dtype=dtype)
+    log(f"full-size {name} {dtype}: M={case.m}")
     offs = gg.expert_offsets_from_recv_counts(case.counts, device=cuda_device)
     case_gpu_a, case_gpu_b = case.a.to(cuda_device), case.b.to(cuda_device)
     ref32 = None
