@@ -43,10 +43,15 @@
  *                                     reference zeroes its counter on the
  *                                     host before each launch, :379-386)
  *   mgg_debug_set_clock_probe      -> no counterpart: a measurement hook
+ *   mgg_debug_counter_slots        -> no counterpart: a test hook
  *   mgg_debug_set_split_flags      -> no counterpart: a test hook (the
  *                                     reference never splits a tile)
  *   mgg_dispatch_layout_noalloc    -> no counterpart: mgg_dispatch_layout
  *                                     for callers that cannot allocate
+ *   mgg_set_split_last_round,      -> no counterpart: controls of the atomic
+ *   mgg_reserve_split_workspace,      schedule's split last round (the
+ *   mgg_split_workspace_bytes         reference's atomic kernel, :157-233,
+ *                                     takes whole items)
  */
 #ifndef MGG_H_
 #define MGG_H_
@@ -146,12 +151,16 @@ int mgg_build_work_queue_host(const int64_t* expert_offsets, int64_t num_experts
  * numbered so that each XCD owns a contiguous slice of every round).
  * use_atomic_queue = 1: workers take the next item with an atomic add on a
  * 64-bit counter word owned by the library: one per (device, stream) for
- * direct launches, and one of its own for every launch captured into a HIP
- * graph (so graph replays never share a word with other launches).  The
- * words live in a file-scope device array (no allocation; at most 4096 per
- * device).  Each launch tags the word with a fresh epoch and claims whatever
- * it finds there, so a word left dirty by a launch that did not finish never
- * drops or repeats tiles; the launch's last ticket returns it to zero.
+ * direct launches, and one per (capture, stream) for launches captured into
+ * a HIP graph (so graph replays never share a word with other launches; the
+ * word is released when the graph is destroyed).  The words live in a
+ * file-scope device array (no allocation; at most 4096 held at once per
+ * device).  Each launch tags the word with its epoch (the next in the
+ * word's sequence) and claims whatever other value it finds there, so a
+ * word left dirty by a launch that did not finish never drops or repeats
+ * tiles; the launch's last ticket leaves the word tagged for the next one.
+ * Graph replays of one captured launch are ordered on their stream; one
+ * graph replayed on two streams at once would share its word and race.
  * If work_counter is non-null (device int32) it receives W + G, the value
  * the reference's counter ends at (:379-416: each worker over-fetches once),
  * where W is the queue length of the report tile, report_block_m x
@@ -171,7 +180,7 @@ int mgg_build_work_queue_host(const int64_t* expert_offsets, int64_t num_experts
  * in those columns must be finite (they are multiplied by zeros; the drop-in
  * makes them zeros).
  * (ABI version 4 added report_block_m, report_block_n; version 6 any K for
- * N-major B.)
+ * N-major B; version 7 the split controls and per-capture counter words.)
  */
 int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
                      const int32_t* expert_offsets, int64_t m_size, int64_t k_size, int64_t n_size,
@@ -257,6 +266,13 @@ int mgg_grouped_gemm_fp8(const void* a, const void* b, void* c, const int32_t* e
 int mgg_debug_set_dequeue_counter(uint64_t value, void* stream);
 
 /*
+ * Test hook, no counterpart in the reference: *held = the number of counter
+ * words of `device` now assigned to a stream or to a live graph capture
+ * (words of destroyed graphs are free again).
+ */
+int mgg_debug_counter_slots(int device, int* held);
+
+/*
  * Measurement hook, no counterpart in the reference: while `probe` (device
  * memory, two uint64, caller-zeroed) is set, every grouped-GEMM launch adds,
  * for each of its first eight workgroups, the shader-clock ticks (s_memtime)
@@ -277,6 +293,29 @@ int mgg_debug_set_clock_probe(uint64_t* probe);
  * Enqueued on `stream`.
  */
 int mgg_debug_set_split_flags(uint64_t value, void* stream);
+
+/*
+ * The atomic schedule's split last round, no counterpart in the reference
+ * (its atomic kernel takes whole items).  With the device-derived queue, an
+ * atomic launch whose last round holds at most a quarter (a half) as many
+ * tiles as workers takes each of those tiles as 4 (2) parts of K; the parts'
+ * fp32 sums meet in a per-(device, stream) workspace of one 256 x 256 fp32
+ * slot per CU (64 MiB on a 256-CU device) plus one flag word per CU.  The
+ * sums then round differently in the last bits from the unsplit tile
+ * (striped, graph-captured, or split-off launches of the same call).
+ *
+ * mgg_set_split_last_round(0) turns splitting off process-wide (every tile
+ * whole, bitwise the striped schedule's results); 1 turns it back on (the
+ * default).  mgg_reserve_split_workspace makes the workspace of `stream` on
+ * the current device now, so no launch allocates it (otherwise the first
+ * atomic launch on the stream that could split does); it is never freed.
+ * At most 16 streams per device get one; launches on further streams, and
+ * launches under graph capture, take every tile whole.
+ * mgg_split_workspace_bytes reports the bytes held for `stream` (0: none).
+ */
+int mgg_set_split_last_round(int enabled);
+int mgg_reserve_split_workspace(void* stream);
+int mgg_split_workspace_bytes(void* stream, int64_t* bytes);
 
 /*
  * Dispatch layout of T tokens routed to top_k experts each (one GPU's share):

@@ -4,6 +4,7 @@
 // message for mgg_last_error().
 #include <algorithm>
 #include <atomic>
+#include <deque>
 #include <map>
 #include <mutex>
 #include <string>
@@ -39,24 +40,47 @@ namespace {
 
 thread_local std::string g_last_error;
 
-std::atomic<uint32_t> g_epoch{0};
 std::atomic<unsigned long long*> g_clock_probe{nullptr};
+std::atomic<int> g_split_enabled{1};
 
-uint32_t next_epoch() {
-  uint32_t e = ++g_epoch;
-  while (e == 0) e = ++g_epoch;  // 0 is the value a finished launch leaves
-  return e;
+// Epoch of the seq-th launch on a counter slot: distinct for 2^32 launches,
+// and never 0, the value every word starts at and the likeliest junk.
+uint32_t epoch_of(uint32_t seq) {
+  const uint32_t e = (seq + 1u) * 0x9E3779B1u;
+  return e != 0 ? e : 1u;
 }
 
-// Slots: launches on one (device, stream) share a slot (they run in stream
-// order); a launch captured into a graph gets a slot of its own for good, so
-// replays of the graph never share a word with direct launches on the
-// capture stream or with another captured launch.
+// Counter slots.  Direct launches on one (device, stream) share a slot (they
+// run in stream order), and each launch tags it with the slot's next epoch
+// in sequence and leaves it tagged with the one after, so the next launch
+// finds its own epoch there.  Launches captured into a graph on one stream in
+// one capture share a slot of their own with one fixed epoch (they run in
+// order within the graph, and every replay starts where the last one ended);
+// the slot returns to the device's free list when the graph is destroyed
+// (a user object the graph holds), and freed slots are reused oldest first,
+// after every never-used slot.
+struct CaptureKey {
+  int device;
+  unsigned long long capture_id;
+  hipStream_t stream;
+  bool operator<(const CaptureKey& o) const {
+    if (device != o.device) return device < o.device;
+    if (capture_id != o.capture_id) return capture_id < o.capture_id;
+    return stream < o.stream;
+  }
+};
+struct CapturedSlot {
+  int slot;
+  uint32_t epoch;
+};
 struct CounterSlots {
   std::mutex mu;
   std::map<std::pair<int, hipStream_t>, int> by_stream;
-  std::vector<unsigned long long*> base;  // per device: counter_pool's address there
-  std::vector<int> used;                  // per device: slots handed out
+  std::map<CaptureKey, CapturedSlot> by_capture;
+  std::vector<unsigned long long*> base;      // per device: counter_pool's address there
+  std::vector<int> used;                      // per device: slots ever handed out
+  std::vector<std::deque<int>> freed;         // per device: released slots, oldest first
+  std::vector<std::vector<uint32_t>> seq;     // per device, per slot: launches so far
 };
 CounterSlots g_slots;
 
@@ -64,15 +88,44 @@ int pool_base(int device, unsigned long long** out) {
   if ((int)g_slots.base.size() <= device) {
     g_slots.base.resize(device + 1, nullptr);
     g_slots.used.resize(device + 1, 0);
+    g_slots.freed.resize(device + 1);
+    g_slots.seq.resize(device + 1);
   }
   if (g_slots.base[device] == nullptr) {
     void* ptr = nullptr;
     const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(counter_pool));
     if (err != hipSuccess) return hip_error(err, "hipGetSymbolAddress(counter_pool)");
     g_slots.base[device] = static_cast<unsigned long long*>(ptr);
+    g_slots.seq[device].assign(kCounterSlots, 0u);
   }
   *out = g_slots.base[device];
   return MGG_OK;
+}
+
+// A slot for a new owner (g_slots.mu held): never-used slots first, then the
+// longest-released one; -1 when every slot is held.
+int take_slot(int device) {
+  if (g_slots.used[device] < kCounterSlots) return g_slots.used[device]++;
+  if (!g_slots.freed[device].empty()) {
+    const int s = g_slots.freed[device].front();
+    g_slots.freed[device].pop_front();
+    return s;
+  }
+  return -1;
+}
+
+// Destructor of the user object a capturing graph holds: its slot is free.
+void release_captured_slot(void* arg) {
+  CaptureKey* key = static_cast<CaptureKey*>(arg);
+  {
+    std::lock_guard<std::mutex> lock(g_slots.mu);
+    auto it = g_slots.by_capture.find(*key);
+    if (it != g_slots.by_capture.end()) {
+      g_slots.freed[key->device].push_back(it->second.slot);
+      g_slots.by_capture.erase(it);
+    }
+  }
+  delete key;
 }
 
 // scratch's device address on the current device, looked up once per device
@@ -96,34 +149,88 @@ int scratch_for_current_device(int32_t** out) {
   return MGG_OK;
 }
 
-// The counter word for a launch on `stream` (current device).
-int counter_for(hipStream_t stream, unsigned long long** out) {
+// The counter word for a launch on `stream` (current device), the launch's
+// epoch and the epoch it leaves in the word for the slot's next launch.
+// `count_launch` false: only the word (the debug hook).
+int counter_for(hipStream_t stream, unsigned long long** out, uint32_t* epoch, uint32_t* next,
+                bool count_launch = true) {
   int device = 0;
   hipError_t err = hipGetDevice(&device);
   if (err != hipSuccess) return hip_error(err, "hipGetDevice");
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  unsigned long long capture_id = 0;
+  hipGraph_t graph = nullptr;
   if (stream != nullptr) {
-    err = hipStreamIsCapturing(stream, &capture);
-    if (err != hipSuccess) return hip_error(err, "hipStreamIsCapturing");
+    const hipGraphNode_t* deps = nullptr;
+    size_t num_deps = 0;
+    err = hipStreamGetCaptureInfo_v2(stream, &capture, &capture_id, &graph, &deps, &num_deps);
+    if (err != hipSuccess) return hip_error(err, "hipStreamGetCaptureInfo_v2");
   }
-  std::lock_guard<std::mutex> lock(g_slots.mu);
   unsigned long long* base = nullptr;
-  const int rc = pool_base(device, &base);
-  if (rc != MGG_OK) return rc;
-  const auto key = std::make_pair(device, stream);
-  if (capture == hipStreamCaptureStatusNone) {
+  if (capture == hipStreamCaptureStatusNone || !count_launch) {
+    std::lock_guard<std::mutex> lock(g_slots.mu);
+    int rc = pool_base(device, &base);
+    if (rc != MGG_OK) return rc;
+    const auto key = std::make_pair(device, stream);
     auto it = g_slots.by_stream.find(key);
+    int slot;
     if (it != g_slots.by_stream.end()) {
-      *out = base + it->second;
+      slot = it->second;
+    } else {
+      slot = take_slot(device);
+      if (slot < 0)
+        return set_error(MGG_ERR_UNSUPPORTED,
+                         "atomic queue: more than 4096 streams and live captures on one device");
+      g_slots.by_stream.emplace(key, slot);
+    }
+    *out = base + slot;
+    if (count_launch) {
+      uint32_t& s = g_slots.seq[device][slot];
+      *epoch = epoch_of(s);
+      *next = epoch_of(s + 1);
+      ++s;
+    }
+    return MGG_OK;
+  }
+  const CaptureKey key{device, capture_id, stream};
+  bool fresh = false;
+  int slot = -1;
+  {
+    std::lock_guard<std::mutex> lock(g_slots.mu);
+    int rc = pool_base(device, &base);
+    if (rc != MGG_OK) return rc;
+    auto it = g_slots.by_capture.find(key);
+    if (it != g_slots.by_capture.end()) {
+      *out = base + it->second.slot;
+      *epoch = *next = it->second.epoch;
       return MGG_OK;
     }
+    slot = take_slot(device);
+    if (slot < 0)
+      return set_error(MGG_ERR_UNSUPPORTED,
+                       "atomic queue: more than 4096 streams and live captures on one device");
+    // The slot's next epoch in sequence: different from whatever its last
+    // owner left in the word.
+    const uint32_t e = epoch_of(g_slots.seq[device][slot]++);
+    g_slots.by_capture.emplace(key, CapturedSlot{slot, e});
+    *out = base + slot;
+    *epoch = *next = e;
+    fresh = true;
   }
-  if (g_slots.used[device] >= kCounterSlots)
-    return set_error(MGG_ERR_UNSUPPORTED,
-                     "atomic queue: more than 4096 streams and captured launches on one device");
-  const int slot = g_slots.used[device]++;
-  if (capture == hipStreamCaptureStatusNone) g_slots.by_stream.emplace(key, slot);
-  *out = base + slot;
+  if (fresh && graph != nullptr) {
+    // The graph holds the only reference: its destruction frees the slot.
+    // Without a user object the slot stays held (the launch still runs).
+    // (If the graph cannot take the object, it and the slot stay held.)
+    CaptureKey* arg = new CaptureKey(key);
+    hipUserObject_t obj = nullptr;
+    if (hipUserObjectCreate(&obj, arg, release_captured_slot, 1, hipUserObjectNoDestructorSync) !=
+        hipSuccess) {
+      (void)hipGetLastError();
+      delete arg;
+    } else if (hipGraphRetainUserObject(graph, obj, 1, hipGraphUserObjectMove) != hipSuccess) {
+      (void)hipGetLastError();
+    }
+  }
   return MGG_OK;
 }
 
@@ -131,17 +238,18 @@ int counter_for(hipStream_t stream, unsigned long long** out) {
 // fp32 partial sums in uncached memory (a part written on one XCD is read on
 // another, and no cache level may hold a stale copy) and zeroed flag words,
 // one slot and one flag word per work item of a split tile (a tile of s parts
-// uses s slots and s - 1 flags).  Made on the first atomic launch on a stream
-// that could split, for as many BM x BN slots as it has workers (a split
-// touches at most that many), and replaced by a larger one when a later
-// launch needs more.
-// None is ever freed: uncached memory a kernel has read must stay allocated
-// until the process ends, and a replaced workspace may still be in use by
-// launches queued before it.  A launch under graph capture gets none (it
-// takes every tile whole), so capture never allocates.  At most
-// kMaxSplitSpaces streams per device get one (64 MiB each at 256 workers of
-// 256x256 tiles); launches on further streams take every tile whole.
+// uses s slots and s - 1 flags).  A split never has more work items than the
+// launch has workers and happens only when they fit in the slots, so the
+// workspace holds one 256 x 256 slot (the largest tile) per CU and no
+// more: 64 MiB on a 256-CU device, whatever the launch's worker count or
+// tile.  It is made once, by mgg_reserve_split_workspace or the stream's
+// first atomic launch that could split, and never replaced or freed
+// (uncached memory a kernel has read must stay allocated until the process
+// ends).  A launch under graph capture gets none (it takes every tile
+// whole), so capture never allocates.  At most kMaxSplitSpaces streams per
+// device get one; launches on further streams take every tile whole.
 constexpr int kMaxSplitSpaces = 16;
+constexpr int64_t kSplitSlotBytes = 256 * 256 * 4;
 struct SplitSpace {
   float* partials = nullptr;
   unsigned long long* flags = nullptr;
@@ -151,50 +259,68 @@ struct SplitSpace {
 std::mutex g_split_mu;
 std::map<std::pair<int, hipStream_t>, SplitSpace> g_split;
 
-// Sets p's split fields for a launch of `workers` workgroups of BM x BN
-// tiles on `stream`, or leaves them null when no workspace can be had.
-int split_space_for(hipStream_t stream, int workers, int block_m, int block_n, GemmParams* p) {
+// The workspace of (current device, stream), made if `create` and possible;
+// *out is null when there is none.
+int split_space(hipStream_t stream, bool create, const SplitSpace** out) {
+  *out = nullptr;
   int device = 0;
   hipError_t err = hipGetDevice(&device);
   if (err != hipSuccess) return hip_error(err, "hipGetDevice");
+  const auto key = std::make_pair(device, stream);
+  std::lock_guard<std::mutex> lock(g_split_mu);
+  auto it = g_split.find(key);
+  if (it != g_split.end()) {
+    *out = &it->second;
+    return MGG_OK;
+  }
+  if (!create) return MGG_OK;
+  int on_device = 0;
+  for (const auto& kv : g_split) on_device += kv.first.first == device ? 1 : 0;
+  if (on_device >= kMaxSplitSpaces) return MGG_OK;
+  int cus = 0;
+  err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+  if (err != hipSuccess) return hip_error(err, "hipDeviceGetAttribute(MultiprocessorCount)");
+  const int64_t words = cus > 0 ? cus : 1;
+  const int64_t bytes = words * kSplitSlotBytes;
+  void* partials = nullptr;
+  void* flags = nullptr;
+  if (hipExtMallocWithFlags(&partials, (size_t)bytes, hipDeviceMallocUncached) != hipSuccess) {
+    (void)hipGetLastError();  // no workspace: launches take every tile whole
+    return MGG_OK;
+  }
+  if (hipMalloc(&flags, (size_t)words * 8) != hipSuccess) {
+    (void)hipGetLastError();  // (the uncached block stays allocated, unused)
+    return MGG_OK;
+  }
+  err = hipMemsetAsync(flags, 0, (size_t)words * 8, stream);
+  if (err != hipSuccess) return hip_error(err, "hipMemsetAsync(split flags)");
+  SplitSpace& sp = g_split[key];
+  sp.partials = static_cast<float*>(partials);
+  sp.flags = static_cast<unsigned long long*>(flags);
+  sp.bytes = bytes;
+  sp.flag_words = words;
+  *out = &sp;
+  return MGG_OK;
+}
+
+// Sets p's split fields for a launch of BM x BN tiles on `stream`, or leaves
+// them null (every tile whole): splitting turned off, graph capture, or no
+// workspace to be had.
+int split_space_for(hipStream_t stream, int block_m, int block_n, GemmParams* p) {
+  if (!g_split_enabled.load()) return MGG_OK;
   if (stream != nullptr) {
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-    err = hipStreamIsCapturing(stream, &capture);
+    const hipError_t err = hipStreamIsCapturing(stream, &capture);
     if (err != hipSuccess) return hip_error(err, "hipStreamIsCapturing");
     if (capture != hipStreamCaptureStatusNone) return MGG_OK;
   }
+  const SplitSpace* sp = nullptr;
+  const int rc = split_space(stream, true, &sp);
+  if (rc != MGG_OK || sp == nullptr) return rc;
   const int64_t slot_bytes = (int64_t)block_m * block_n * 4;
-  const int64_t need_bytes = (int64_t)workers * slot_bytes;
-  const int64_t need_flags = workers;
-  std::lock_guard<std::mutex> lock(g_split_mu);
-  const auto key = std::make_pair(device, stream);
-  if (g_split.find(key) == g_split.end()) {
-    int on_device = 0;
-    for (const auto& kv : g_split) on_device += kv.first.first == device ? 1 : 0;
-    if (on_device >= kMaxSplitSpaces) return MGG_OK;
-  }
-  SplitSpace& sp = g_split[key];
-  if (sp.bytes < need_bytes || sp.flag_words < need_flags) {
-    const int64_t bytes = std::max(need_bytes, sp.bytes);
-    const int64_t words = std::max(need_flags, sp.flag_words);
-    void* partials = nullptr;
-    void* flags = nullptr;
-    if (hipExtMallocWithFlags(&partials, (size_t)bytes, hipDeviceMallocUncached) != hipSuccess ||
-        hipMalloc(&flags, (size_t)words * 8) != hipSuccess) {
-      (void)hipGetLastError();  // no workspace: this launch takes every tile whole
-      return MGG_OK;             // (a partial allocation stays unused)
-    }
-    err = hipMemsetAsync(flags, 0, (size_t)words * 8, stream);
-    if (err != hipSuccess) return hip_error(err, "hipMemsetAsync(split flags)");
-    sp.partials = static_cast<float*>(partials);
-    sp.flags = static_cast<unsigned long long*>(flags);
-    sp.bytes = bytes;
-    sp.flag_words = words;
-  }
-  p->split_partials = sp.partials;
-  p->split_flags = sp.flags;
-  const int64_t slots = std::min(sp.bytes / slot_bytes, sp.flag_words);
-  p->split_slots = (int32_t)std::min<int64_t>(slots, (int64_t)1 << 30);
+  p->split_partials = sp->partials;
+  p->split_flags = sp->flags;
+  p->split_slots = (int32_t)std::min<int64_t>(sp->bytes / slot_bytes, sp->flag_words);
   return MGG_OK;
 }
 
@@ -220,7 +346,7 @@ using mgg::set_error;
 
 extern "C" {
 
-int mgg_abi_version(void) { return 6; }
+int mgg_abi_version(void) { return 7; }
 
 const char* mgg_last_error(void) { return mgg::g_last_error.c_str(); }
 
@@ -464,12 +590,11 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   p.a_rows = a_rows;
   p.a_src_rows = a_rows != nullptr ? a_src_rows : 0;
   if (p.atomic) {
-    int rc = counter_for(st, &p.counter);
+    int rc = counter_for(st, &p.counter, &p.epoch, &p.next_epoch);
     if (rc != MGG_OK) return rc;
-    p.epoch = next_epoch();
     p.report = work_counter;
     if (num_work < 0 && k_size > 0) {
-      rc = split_space_for(st, workers, block_m, block_n, &p);
+      rc = split_space_for(st, block_m, block_n, &p);
       if (rc != MGG_OK) return rc;
     }
   }
@@ -551,29 +676,52 @@ int mgg_debug_set_dequeue_counter(uint64_t value, void* stream) {
   mgg::clear_error();
   unsigned long long* word = nullptr;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  const int rc = mgg::counter_for(st, &word);
+  uint32_t unused_epoch = 0, unused_next = 0;
+  const int rc = mgg::counter_for(st, &word, &unused_epoch, &unused_next, false);
   if (rc != MGG_OK) return rc;
   return mgg::launch_fill_u64(word, 1, (unsigned long long)value, st);
 }
 
 int mgg_debug_set_split_flags(uint64_t value, void* stream) {
   mgg::clear_error();
-  int device = 0;
-  const hipError_t err = hipGetDevice(&device);
-  if (err != hipSuccess) return mgg::hip_error(err, "hipGetDevice");
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  unsigned long long* flags = nullptr;
-  int64_t words = 0;
-  {
-    std::lock_guard<std::mutex> lock(mgg::g_split_mu);
-    const auto it = mgg::g_split.find(std::make_pair(device, st));
-    if (it != mgg::g_split.end()) {
-      flags = it->second.flags;
-      words = it->second.flag_words;
-    }
-  }
-  if (flags == nullptr) return set_error(MGG_ERR_INVALID, "no split workspace on this stream yet");
-  return mgg::launch_fill_u64(flags, (int)words, (unsigned long long)value, st);
+  const mgg::SplitSpace* sp = nullptr;
+  const int rc = mgg::split_space(st, false, &sp);
+  if (rc != MGG_OK) return rc;
+  if (sp == nullptr) return set_error(MGG_ERR_INVALID, "no split workspace on this stream yet");
+  return mgg::launch_fill_u64(sp->flags, (int)sp->flag_words, (unsigned long long)value, st);
+}
+
+int mgg_debug_counter_slots(int device, int* held) {
+  mgg::clear_error();
+  if (held == nullptr) return set_error(MGG_ERR_INVALID, "held is null");
+  std::lock_guard<std::mutex> lock(mgg::g_slots.mu);
+  *held = 0;
+  if (device >= 0 && device < (int)mgg::g_slots.used.size())
+    *held = mgg::g_slots.used[device] - (int)mgg::g_slots.freed[device].size();
+  return MGG_OK;
+}
+
+int mgg_reserve_split_workspace(void* stream) {
+  mgg::clear_error();
+  const mgg::SplitSpace* sp = nullptr;
+  return mgg::split_space(static_cast<hipStream_t>(stream), true, &sp);
+}
+
+int mgg_split_workspace_bytes(void* stream, int64_t* bytes) {
+  mgg::clear_error();
+  if (bytes == nullptr) return set_error(MGG_ERR_INVALID, "bytes is null");
+  const mgg::SplitSpace* sp = nullptr;
+  const int rc = mgg::split_space(static_cast<hipStream_t>(stream), false, &sp);
+  if (rc != MGG_OK) return rc;
+  *bytes = sp != nullptr ? sp->bytes + sp->flag_words * 8 : 0;
+  return MGG_OK;
+}
+
+int mgg_set_split_last_round(int enabled) {
+  mgg::clear_error();
+  mgg::g_split_enabled.store(enabled ? 1 : 0);
+  return MGG_OK;
 }
 
 int64_t mgg_dispatch_layout_workspace_bytes(int64_t num_tokens, int top_k, int64_t num_experts) {

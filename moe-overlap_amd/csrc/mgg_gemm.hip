@@ -263,14 +263,16 @@ __device__ int32_t queue_length(const GemmParams& p, int bm, int n_tiles, int32_
   return total;
 }
 
-// Dequeue tickets of the atomic schedule from a 64-bit word (epoch << 32) |
-// count, where `epoch` is this launch's tag (never 0).  A launch that runs to
-// its end leaves the word at 0; one that does not (an aborted process, a
-// caller that overwrote the memory) may leave any value.  A worker's first
-// ticket therefore claims the word: it reads it and, unless the word already
-// carries this launch's epoch, swaps in (epoch, 1) and holds ticket 0; a
-// worker that loses the swap to another claim takes an ordinary ticket.
-// Every later ticket is one atomic add.  Called by one lane per workgroup.
+// Dequeue tickets of the atomic schedule come from a 64-bit word (epoch << 32)
+// | count, where `epoch` is this launch's tag.  A launch that runs to its end
+// leaves the word at (next_epoch << 32) | 0, next_epoch being the tag the
+// host gives the next launch on the same word, so that launch's tickets are
+// plain atomic adds.  A word holding another epoch (a launch that did not
+// finish, a caller that overwrote the memory, a reused word) is claimed: the
+// worker that finds it reads it and, unless it already carries this launch's
+// epoch, swaps in (epoch, 1) and holds ticket 0; a worker that loses the
+// swap to another claim takes an ordinary ticket.  Called by one lane per
+// workgroup.
 __device__ __forceinline__ int32_t first_ticket(unsigned long long* word, uint32_t epoch) {
   const unsigned long long tagged = ((unsigned long long)epoch << 32) | 1ull;
   unsigned long long cur = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -286,9 +288,10 @@ __device__ __forceinline__ int32_t first_ticket(unsigned long long* word, uint32
     cur = seen;
   }
 }
-__device__ __forceinline__ int32_t next_ticket(unsigned long long* word, uint32_t epoch) {
-  const unsigned long long t = atomicAdd(word, 1ull);
-  if ((uint32_t)(t >> 32) == epoch) return (int32_t)(uint32_t)t;
+// The ticket held by `raw`, the value an atomic add of 1 on the word returned.
+__device__ __forceinline__ int32_t ticket_from(unsigned long long raw, unsigned long long* word,
+                                               uint32_t epoch) {
+  if ((uint32_t)(raw >> 32) == epoch) return (int32_t)(uint32_t)raw;
   return first_ticket(word, epoch);
 }
 
@@ -319,7 +322,6 @@ __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t soff, 
                : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds)
                : "memory", "m0");
 }
-#pragma clang diagnostic pop
 // One 4-byte-per-lane DMA: lane l's word lands at LDS byte address lds + 4*l.
 __device__ __forceinline__ void dma4(i32x4 rsrc, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds"
@@ -327,6 +329,7 @@ __device__ __forceinline__ void dma4(i32x4 rsrc, uint32_t voff, uint32_t lds) {
                : "v"(voff), "s"(rsrc), "s"(lds)
                : "memory", "m0");
 }
+#pragma clang diagnostic pop
 // Waits until at most N of this wave's DMAs are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_dma() {
@@ -482,19 +485,22 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // first G take one ticket each (W - G of them when W > G) and every worker
   // with a first item (min(W, G) of them) draws one ticket past the queue
   // before it stops, so the worker that draws ticket W-1 is the last to touch
-  // the counter: it returns the word to 0 for the next launch and hands the
+  // the counter: it tags the word with the next launch's epoch and hands the
   // caller's work_counter the value the reference's counter ends at (W + G,
-  // for the report tile's queue length).  Drawn by lane 0 only.
-  bool claimed = false;
-  auto draw = [&]() -> int32_t {
-    const int32_t t = claimed ? next_ticket(p.counter, p.epoch) : first_ticket(p.counter, p.epoch);
-    claimed = true;
+  // for the report tile's queue length).  Drawn by lane 0 only, in two
+  // halves: the atomic add is issued inside a tile's K loop and its value is
+  // looked at only once the tile's K loop is done (a branch on it inside the
+  // loop would make the wave wait for every DMA it has in flight).
+  auto resolve = [&](unsigned long long raw) -> int32_t {
+    const int32_t t = ticket_from(raw, p.counter, p.epoch);
     if (t == W - 1) {
-      __hip_atomic_store(p.counter, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.counter, (unsigned long long)p.next_epoch << 32, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
       if (p.report != nullptr) atomicExch(p.report, w_report + G);
     }
     return G + t;
   };
+  auto draw = [&]() -> int32_t { return resolve(atomicAdd(p.counter, 1ull)); };
   // K < 2^30 (the host bounds (K+8)*ldb_k*2 below 2^31), so stage positions
   // are 32-bit and the full/partial decision stays in scalar registers.
   // K extent of the tile being issued (set by set_sources): all of K, or one
@@ -653,10 +659,14 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // tile c (ordinary loads, issued ahead of their use), then turn them into
   // the lane's DMA offsets.  Rows past the tile's valid rows, and indices
   // outside the source matrix, get offsets past the descriptor (zeros).
+  // Only entries inside [0, M) of the index array are read: a tile whose
+  // rows fall outside it (offsets past M or negative) gets zero rows.
   auto load_rows = [&](const Coords& c) {
 #pragma unroll
-    for (int t = 0; t < kAPerWave; ++t)
-      a_tok[t] = a_row(t) < c.rows_valid ? p.a_rows[c.row_base + a_row(t)] : -1;
+    for (int t = 0; t < kAPerWave; ++t) {
+      const int64_t r = c.row_base + a_row(t);
+      a_tok[t] = a_row(t) < c.rows_valid && r >= 0 && r < p.m ? p.a_rows[r] : -1;
+    }
   };
   auto set_a_rows = [&]() {
 #pragma unroll
@@ -1014,7 +1024,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       for (int st = 1; st < kLB; ++st) issue_bstage(st, 0, kBPerWave);
   };
 
-  auto main_loop = [&](bool take_ticket, int32_t& ticket) {
+  auto main_loop = [&](bool take_ticket, unsigned long long& ticket) {
 #pragma unroll
     for (int i = 0; i < kNB; ++i)
 #pragma unroll
@@ -1027,8 +1037,9 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       wait_stage(0, issued);
     __syncthreads();
     // The next tile's ticket, taken after the first wait so that this
-    // wave's first DMA wait does not also wait for the atomic.
-    if (take_ticket && tid == 0) ticket = draw();
+    // wave's first DMA wait does not also wait for the atomic; its value is
+    // resolved after the K loop.
+    if (take_ticket && tid == 0) ticket = atomicAdd(p.counter, 1ull);
     if constexpr (kABlk) {
       read_kstep_ab(IntConst<0>{}, 0, 0, 0, 0);
       read_kstep_ab(IntConst<0>{}, 0, 0, 0, 1);
@@ -1343,10 +1354,10 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       if (s < nk) issue_stage(issued = s);
   }
   for (;;) {
-    int32_t ticket = 0;
+    unsigned long long ticket = 0;
     main_loop(p.atomic != 0, ticket);
     // The next item: the ticket taken during this tile, or the next stripe.
-    if (p.atomic && tid == 0) *s_item = ticket;
+    if (p.atomic && tid == 0) *s_item = resolve(ticket);
     __syncthreads();  // every wave is done reading this tile's LDS stages; s_item is visible
     int32_t next = p.atomic ? *s_item : w + G;
     // A split part meets the others before anything of the next item is
@@ -1453,6 +1464,11 @@ grouped_gemm_kernel(GemmParams p) {
                               rep_tiles, &w_report);
   }
   if (W == 0) {
+    // No ticket is drawn: the counter word is handed on to the next launch
+    // as the last ticket would have left it.
+    if (p.atomic && blockIdx.x == 0 && threadIdx.x == 0)
+      __hip_atomic_store(p.counter, (unsigned long long)p.next_epoch << 32, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     zero_fill(p, (EPI & 3) == kEpiSwiglu ? p.n / 2 : p.n);
     return;
   }

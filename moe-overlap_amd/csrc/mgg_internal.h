@@ -44,7 +44,8 @@ struct GemmParams {
   const int32_t* q_tile_n;
   // Atomic mode: the library's dequeue counter, a 64-bit word (epoch << 32) |
   // count.  A word whose epoch is not this launch's is left over from another
-  // launch (any count) and is claimed afresh as count 0.
+  // launch (any count) and is claimed afresh as count 0; the launch's last
+  // ticket leaves it at (next_epoch << 32) | 0.
   unsigned long long* counter;
   int32_t* report;   // atomic mode: caller's work_counter, receives W_report + G, or null
   int64_t m;
@@ -60,7 +61,8 @@ struct GemmParams {
   int32_t num_work;  // < 0: derive the queue from the offsets on the device
   int32_t atomic;
   int32_t remap_xcd;
-  uint32_t epoch;    // atomic mode: this launch's tag in the counter words (never 0)
+  uint32_t epoch;       // atomic mode: this launch's tag in the counter word and split flags
+  uint32_t next_epoch;  // the tag the last ticket leaves in the counter word (the next launch's)
   // The tile whose queue length W_report the work_counter reports (W_report
   // + G): the caller's requested tile, which may differ from the tile the
   // kernel computes with; the kernel counts it from the offsets.

@@ -39,7 +39,11 @@ Differences, all in arguments that do not change results:
   tile, their fp32 sums added pairwise in a fixed tree: the output can differ
   in the last bits from the striped schedule's (both within the tolerance of
   the fp32 product; each repeats itself bitwise).  Graph-captured launches
-  and prebuilt queues take whole tiles.
+  and prebuilt queues take whole tiles, and ``set_split_last_round(False)``
+  turns the split off (every schedule then gives bitwise the same output).
+  The parts meet in a per-stream workspace of 64 MiB (one 256 x 256 fp32
+  slot per CU) that the stream's first atomic call allocates, unless
+  ``reserve_split_workspace`` made it beforehand.
 * Operands whose inner stride is not 1 or whose rows are not 16-byte aligned
   are copied on the device first.  K not a multiple of 8: A is copied with
   zero columns to the next multiple of 8 and B is read in place (the kernel
@@ -64,6 +68,9 @@ __all__ = [
     "_build_work_queue",
     "grouped_gemm_flops",
     "quantize_fp8_rows",
+    "set_split_last_round",
+    "reserve_split_workspace",
+    "split_workspace_bytes",
 ]
 
 # Tiles compiled into libmgg for bf16/fp16 (fused epilogues: 256x256, 128x128).
@@ -91,6 +98,33 @@ def _cu_count(dev_index: int) -> int:
     if n is None:
         n = _CU_COUNTS[dev_index] = _nat.device_cu_count(dev_index)
     return n
+
+
+def set_split_last_round(enabled: bool) -> None:
+    """Turns the atomic schedule's split last round on (the default) or off,
+    process-wide.  Off, every tile is summed whole, so an atomic call gives
+    bitwise the striped (and graph-captured) call's output."""
+    _nat.check(_nat.lib().mgg_set_split_last_round(1 if enabled else 0))
+
+
+def reserve_split_workspace(device: Optional[torch.device] = None) -> None:
+    """Makes the split-round workspace of the current stream of `device` now
+    (64 MiB on MI355X, never freed), so that no later atomic call on that
+    stream allocates device memory."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    dev_index = dev.index if dev.index is not None else torch.cuda.current_device()
+    with torch.cuda.device(dev_index):
+        _nat.check(_nat.lib().mgg_reserve_split_workspace(_stream_handle(dev)))
+
+
+def split_workspace_bytes(device: Optional[torch.device] = None) -> int:
+    """Bytes of split-round workspace held for the current stream of `device`."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    dev_index = dev.index if dev.index is not None else torch.cuda.current_device()
+    n = ctypes.c_int64(0)
+    with torch.cuda.device(dev_index):
+        _nat.check(_nat.lib().mgg_split_workspace_bytes(_stream_handle(dev), ctypes.byref(n)))
+    return int(n.value)
 
 
 # --------------------------------------------------------------------------

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime this library must share)
 
 LIB_PATH = Path(__file__).resolve().parent / "libmgg.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 MGG_OK = 0
 MGG_ERR_INVALID = 1
@@ -86,6 +86,10 @@ _SIGNATURES = {
     "mgg_debug_set_dequeue_counter": [ctypes.c_uint64, _c_ptr],
     "mgg_debug_set_clock_probe": [_c_ptr],
     "mgg_debug_set_split_flags": [ctypes.c_uint64, _c_ptr],
+    "mgg_debug_counter_slots": [_c_i32, ctypes.POINTER(_c_i32)],
+    "mgg_reserve_split_workspace": [_c_ptr],
+    "mgg_split_workspace_bytes": [_c_ptr, ctypes.POINTER(_c_i64)],
+    "mgg_set_split_last_round": [_c_i32],
     "mgg_dispatch_layout": [
         _c_ptr, _c_i32, _c_i64, _c_i32, _c_i64,  # topk_idx, idx_type, T, top_k, E
         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,  # counts, offsets, slot_pos, token_index, row_assign

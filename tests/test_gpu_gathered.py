@@ -108,3 +108,30 @@ def test_gathered_out_of_range_rows_read_zeros(cuda_device):
         torch.cuda.synchronize()
         assert torch.equal(got, want), atomic
         assert torch.count_nonzero(got[bad.to(cuda_device)]) == 0
+
+
+def test_gathered_offsets_past_m_read_only_m_indices(cuda_device):
+    """Expert offsets that run past M (offsets[E] > m_size) cover only the
+    first M rows: the launch reads no index at or past M (the index array here
+    is longer, so the launch stays inside it either way) and rows < M equal
+    the explicit gather's, which clamps A's rows at M."""
+    counts, t, k, n = [200, 90], 300, 264, 256
+    m = 250  # offsets end at 290
+    gen = torch.Generator().manual_seed(8)
+    x = torch.randn(t, k, generator=gen).to(torch.bfloat16).to(cuda_device)
+    rows = torch.randint(0, t, (sum(counts) + 64,), generator=gen, dtype=torch.int32)
+    rows = rows.to(cuda_device)
+    w = (torch.randn(2, k, n, generator=gen) / math.sqrt(k)).to(torch.bfloat16).to(cuda_device)
+    offs = torch.tensor(orc.expert_offsets_from_recv_counts(counts), dtype=torch.int32,
+                        device=cuda_device)
+    xg = x[rows[:m].long()].contiguous()
+    for atomic in (0, 1):
+        log(f"gathered offsets past M atomic={atomic}")
+        got = torch.full((m, n), float("nan"), dtype=x.dtype, device=cuda_device)
+        nat.check(nat.lib().mgg_grouped_gemm_gathered(
+            nat.MGG_DTYPE_BF16, nat.MGG_EPI_NONE, x.data_ptr(), rows.data_ptr(), t, w.data_ptr(),
+            got.data_ptr(), offs.data_ptr(), m, k, n, 2, x.stride(0), w.stride(0), w.stride(1),
+            got.stride(0), 0, atomic, torch.cuda.current_stream().cuda_stream))
+        want = explicit(xg, w, offs, nat.MGG_EPI_NONE, n, 0, atomic)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), atomic

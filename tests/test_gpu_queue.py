@@ -11,8 +11,11 @@ Reference behaviour pinned here (src/triton_grouped_gemm.py):
 * :369-371  an empty queue zero-fills and leaves the counter untouched.
 Tolerance as in test_gpu_gemm: max |C - C_fp64| <= 2e-2 * sqrt(max(K, 512) / 512).
 """
+import ctypes
+import gc
 import math
 import sys
+import time
 
 import numpy as np
 import pytest
@@ -121,7 +124,7 @@ def test_dirty_counter_word_is_reclaimed(cuda_device, poison):
             torch.cuda.synchronize()
             assert counter.item() == w + g_workers
             assert_parity(c, a, b, offs, k)
-            # A clean launch right after (the dirty one left the word at zero).
+            # A clean launch right after (the dirty one left the word tagged for it).
             counter.zero_()
             c2 = gg.persistent_grouped_gemm(a, b, offs, num_sms=g_workers, block_m=256,
                                             block_n=256, work_counter=counter)
@@ -229,3 +232,44 @@ def test_fp8_and_fused_entry_points_above_2048_experts(cuda_device):
     rel = ((c8.float()[mask] - ref8[mask]).norm() / ref8[mask].norm()).item()
     assert rel <= 1e-2, rel
     assert counter.item() == queue_len(offs, n, 128, 128) + 64
+
+
+def _held_slots(device):
+    n = ctypes.c_int(0)
+    nat.check(nat.lib().mgg_debug_counter_slots(device.index or 0, ctypes.byref(n)))
+    return n.value
+
+
+def test_captured_launches_share_and_release_counter_words(cuda_device):
+    """Atomic launches captured on one stream in one capture share one counter
+    word (40 captures of two launches hold 40 words), every replay is right,
+    and destroying the graphs frees their words, so captures never use up the
+    device's 4096."""
+    a, b, offs = make_inputs([300, 0, 257, 40], 192, 256, torch.bfloat16, cuda_device, seed=9)
+    eager = gg.persistent_grouped_gemm(a, b, offs, use_atomic_queue=False)
+    torch.cuda.synchronize()
+    base = _held_slots(cuda_device)
+    graphs, outs = [], []
+    for _ in range(40):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            o1 = gg.persistent_grouped_gemm(a, b, offs, use_atomic_queue=True)
+            o2 = gg.persistent_grouped_gemm(a, b, offs, use_atomic_queue=True)
+        graphs.append(graph)
+        outs.append((o1, o2))
+    held = _held_slots(cuda_device)
+    log(f"counter words held: {base} before, {held} with 40 graphs")
+    assert held == base + 40
+    for rep in range(2):
+        for graph in graphs:
+            graph.replay()
+        torch.cuda.synchronize()
+        for o1, o2 in outs:
+            assert torch.equal(o1, eager) and torch.equal(o2, eager), rep
+    del graphs, graph, outs, o1, o2
+    gc.collect()
+    torch.cuda.synchronize()
+    deadline = time.time() + 5
+    while _held_slots(cuda_device) != base and time.time() < deadline:
+        time.sleep(0.05)
+    assert _held_slots(cuda_device) == base

@@ -163,3 +163,65 @@ def test_split_fp8(cuda_device):
         assert np.all(np.abs(got - ref) <= 2 ** -8 * np.abs(ref) + 2 ** -16 * mag)
         outs.append(c)
     assert torch.equal(outs[0], outs[1])
+
+
+def test_split_switched_off_takes_whole_tiles(cuda_device):
+    """set_split_last_round(False): the atomic call takes every tile whole and
+    gives the striped call's bits; switched back on it splits again."""
+    counts, k, n, g = CASES[0]
+    a, b, offs = make_inputs(counts, k, n, torch.bfloat16, cuda_device, seed=0)
+    striped = gg.persistent_grouped_gemm(a, b, offs, num_sms=g, use_atomic_queue=False)
+    split = gg.persistent_grouped_gemm(a, b, offs, num_sms=g)
+    try:
+        gg.set_split_last_round(False)
+        whole = gg.persistent_grouped_gemm(a, b, offs, num_sms=g)
+    finally:
+        gg.set_split_last_round(True)
+    again = gg.persistent_grouped_gemm(a, b, offs, num_sms=g)
+    torch.cuda.synchronize()
+    assert torch.equal(whole, striped)
+    assert not torch.equal(split, striped)  # 24 tiles of random sums split in 4
+    assert torch.equal(again, split)
+
+
+def test_captured_split_call_agrees_with_eager(cuda_device):
+    """A call that splits eagerly takes whole tiles under graph capture: every
+    replay gives the striped call's bits and agrees with the eager split call
+    within the tolerance (both checked against the oracle)."""
+    counts, k, n, g = CASES[0]
+    a, b, offs = make_inputs(counts, k, n, torch.bfloat16, cuda_device, seed=1)
+    eager = gg.persistent_grouped_gemm(a, b, offs, num_sms=g)
+    striped = gg.persistent_grouped_gemm(a, b, offs, num_sms=g, use_atomic_queue=False)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = gg.persistent_grouped_gemm(a, b, offs, num_sms=g)
+    for rep in range(3):
+        graph.replay()
+        other = gg.persistent_grouped_gemm(a, b, offs, num_sms=g)  # eager split work between
+        torch.cuda.synchronize()
+        log(f"captured split rep={rep}")
+        assert torch.equal(captured, striped), rep
+        assert torch.equal(other, eager), rep
+        err = (captured.float() - eager.float()).abs().max().item()
+        assert err <= tol(k), err
+    assert_parity(eager, a, b, offs, k)
+    assert_parity(captured, a, b, offs, k)
+
+
+def test_split_workspace_is_one_slot_per_cu(cuda_device):
+    """The split workspace of a stream holds one 256 x 256 fp32 slot and one
+    flag word per CU, whatever the worker count: 64 MiB on a 256-CU device
+    after a num_sms=1000 call (24 tiles in 4 parts), and reserving it again
+    changes nothing."""
+    counts, k, n = [300, 0, 257, 1, 600], 1032, 520
+    a, b, offs = make_inputs(counts, k, n, torch.bfloat16, cuda_device, seed=2)
+    gg.reserve_split_workspace(cuda_device)
+    c = gg.persistent_grouped_gemm(a, b, offs, num_sms=1000)
+    torch.cuda.synchronize()
+    assert_parity(c, a, b, offs, k)
+    cus = gg._cu_count(cuda_device.index or 0)
+    want = cus * (256 * 256 * 4 + 8)
+    assert gg.split_workspace_bytes(cuda_device) == want
+    assert want <= 64 * 2 ** 20 + 8 * 256 or cus > 256
+    gg.reserve_split_workspace(cuda_device)
+    assert gg.split_workspace_bytes(cuda_device) == want
