@@ -23,6 +23,15 @@ Protocol:
    clock keeps drifting down under sustained load, so these read a little
    slower than the timed steps), and a pass of 50 more the kernel's own
    average shader clock (``clock``).
+4. ``flushed``: 50 launches, each after a 512 MiB device write that evicts L2
+   and the 256 MB MALL, HIP events around each launch only: the cache-cold
+   time per launch with its own roofline fraction.
+
+``--experts/--tokens-per-expert/--k/--n/--dtype`` (the reference benchmark
+script's knobs; ``--num-routed-experts``, ``--hidden-size`` and
+``--ffn-size`` are accepted as its names) time a uniform problem of that
+shape instead, and ``--workload reference_bench`` the script's default (E=256
+x 128 tokens, K=7168, N=2048).
 
 Extra fields compare striped and atomic scheduling under uniform and skewed
 routing, the reference's explicit 128x128 request, a cache-cold launch, the
@@ -56,9 +65,17 @@ def parse_args():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--workload", default="uniform",
-                   choices=["uniform", "skewed", "cpu_plumbing", "expert_mlp", "fp8"],
-                   help="uniform (the metric's config), skewed, cpu_plumbing; expert_mlp and fp8 "
+                   choices=["uniform", "skewed", "cpu_plumbing", "reference_bench", "expert_mlp", "fp8"],
+                   help="uniform (the metric's config), skewed, cpu_plumbing, reference_bench (the "
+                        "reference benchmark script's default problem); expert_mlp and fp8 "
                         "time the benchmark expert-MLP forward / fp8 GEMM configs instead")
+    # The reference benchmark script's problem knobs (src/bench_triton_grouped_gemm.py:11-27):
+    # a uniform problem, each unset one taken from the --workload's shape.
+    p.add_argument("--experts", "--num-routed-experts", dest="experts", type=int, default=None)
+    p.add_argument("--tokens-per-expert", type=int, default=None)
+    p.add_argument("--k", "--hidden-size", dest="k", type=int, default=None)
+    p.add_argument("--n", "--ffn-size", dest="n", type=int, default=None)
+    p.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
     # atomic by default, as the reference's API (persistent_grouped_gemm's use_atomic_queue=True,
     # src/triton_grouped_gemm.py:334; its benchmark script makes it opt-in, :28-32); the
     # comparison below times both schedules either way
@@ -85,6 +102,11 @@ def parse_args():
                    help="instead of the GEMM, run --steps plain device copies of this many MiB "
                         "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return p.parse_args()
+
+
+def progress(msg):
+    """A progress line on stderr (the JSON result line goes to stdout)."""
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
 def median(xs):
@@ -417,6 +439,64 @@ def cpu_baseline(case, budget_s):
     }
 
 
+FLUSH_BYTES = 512 * 1024 * 1024  # > the 256 MB MALL + 8 x 4 MB L2
+
+
+def flushed_times_ms(step, dev, launches=50):
+    """Per-launch durations (ms) of `launches` launches, each after a 512 MiB
+    device write that evicts L2 and the MALL (HIP events around the launch
+    only)."""
+    import torch
+
+    scratch = torch.empty(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
+    fill = lambda: scratch.fill_(1.0)
+    event_times_ms(step, 5, flush=fill)
+    t = event_times_ms(step, launches, flush=fill)
+    del scratch
+    return t
+
+
+def reference_bench_summary(dev, dtype, num_sms=None, steps=30):
+    """The reference benchmark script's default problem (E=256 x 128 tokens,
+    K=7168, N=2048, uniform counts; src/bench_triton_grouped_gemm.py:11-17):
+    7.5 GB of weights make it HBM-bound (119 FLOP/B against the bf16 ridge of
+    315).  Warm and flushed kernel times per schedule."""
+    import torch
+
+    import grouped_gemm as gg
+    import workloads
+
+    case = workloads.make_case("reference_bench", device=dev, dtype=dtype)
+    offs = gg.expert_offsets_from_recv_counts(case.counts, device=dev)
+    nbytes = case.algorithmic_bytes()
+    t_hbm = nbytes / (PEAK_HBM_GBPS * 1e9) * 1e3
+    out = {"config": f"E={case.num_experts} x {int(case.counts[0])} tokens, K={case.k}, N={case.n}, "
+                     f"{'bf16' if dtype == torch.bfloat16 else 'fp16'}",
+           "algorithmic_flops": case.flops, "algorithmic_bytes": nbytes,
+           "t_hbm_bound_ms": round(t_hbm, 4), "runs": {}}
+    for mode in ("atomic", "striped"):
+        fn = lambda: gg.persistent_grouped_gemm(case.a, case.b, offs, num_sms=num_sms,
+                                                use_atomic_queue=mode == "atomic")
+        settle_clock(fn)
+        t = median(event_times_ms(fn, steps))
+        tc = median(flushed_times_ms(fn, dev, launches=20))
+        out["runs"][mode] = {"kernel_ms_median": round(t, 4), "tflops": round(case.flops / (t * 1e-3) / 1e12, 1),
+                             "hbm_gbps_at_algorithmic_bytes": round(nbytes / (t * 1e-3) / 1e9, 1),
+                             "frac_of_hbm_roofline": round(t_hbm / t, 4),
+                             "flushed_kernel_ms_median": round(tc, 4),
+                             "flushed_frac_of_hbm_roofline": round(t_hbm / tc, 4)}
+    c = gg.persistent_grouped_gemm(case.a, case.b, offs, num_sms=num_sms)
+    rows = torch.arange(0, case.m, 509, device=dev)
+    e_of = torch.div(rows, int(case.counts[0]), rounding_mode="floor")
+    ref = torch.bmm(case.a[rows].float().unsqueeze(1), case.b[e_of].float()).squeeze(1)
+    out["sampled_rows"] = int(rows.numel())
+    out["max_abs_diff_vs_fp32_sampled"] = round((c[rows].float() - ref).abs().max().item(), 6)
+    out["tolerance"] = round(2e-2 * math.sqrt(case.k / 512), 6)
+    del case, c, ref
+    torch.cuda.empty_cache()
+    return out
+
+
 def _kernel_tile_arg(text):
     if text is None:
         return None
@@ -548,7 +628,21 @@ def main():
     if args.workload in ("expert_mlp", "fp8"):
         secondary_main(args, dev)
         return
-    case = workloads.make_case(args.workload, device=dev, dtype=torch.bfloat16)
+    dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    shape_flags = (args.experts, args.tokens_per_expert, args.k, args.n)
+    if any(v is not None for v in shape_flags):
+        base = workloads.make_case(args.workload, materialize=False)
+        if args.workload not in ("uniform", "reference_bench", "cpu_plumbing"):
+            print("--experts/--tokens-per-expert/--k/--n make a uniform problem: use them with "
+                  "--workload uniform or reference_bench", file=sys.stderr)
+            sys.exit(2)
+        case = workloads.uniform_case(args.experts or base.num_experts,
+                                      args.tokens_per_expert or int(base.counts[0]),
+                                      args.k or base.k, args.n or base.n)
+        workloads.fill_operands(case, device=dev, dtype=dtype)
+    else:
+        case = workloads.make_case(args.workload, device=dev, dtype=dtype)
+    is_metric_config = (case.name == "uniform" and dtype == torch.bfloat16)
     if args.operands == "zero_a":
         case.a.zero_()
     elif args.operands == "zero_b":
@@ -566,6 +660,12 @@ def main():
         return gg.persistent_grouped_gemm(case.a, case.b, offs, **kw)
 
     flops = case.flops
+    nbytes = case.algorithmic_bytes()
+    # MFMA-bound when the problem's FLOP per algorithmic byte is above the
+    # bf16/fp16 ridge (peak FLOP/s over HBM bytes/s), else HBM-bound.
+    hbm_bound = flops / nbytes < PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBPS * 1e9)
+    progress(f"headline {case.name} E={case.num_experts} M={case.m} K={case.k} N={case.n} {args.dtype} "
+             f"{args.mode}: warmup, settle, {args.steps} timed steps")
     r = run_protocol(step, args, flops)
     wall = r["wall_s"]
     if args.profile_only:
@@ -577,14 +677,32 @@ def main():
     k_med = median(kernel_ms)
     k_mean = sum(kernel_ms) / len(kernel_ms)
     k_timed = r["timed_ms_per_launch"]
-    achieved = flops / (k_timed * 1e-3) / 1e12
+    progress(f"timed {k_timed * 1e3:.1f} us per launch; flushed pass")
+    flushed = flushed_times_ms(step, dev)
+    k_flushed = median(flushed)
 
-    # Correctness of the timed configuration against an fp32 torch loop.
+    def roof(ms):
+        if hbm_bound:
+            return nbytes / (ms * 1e-3) / 1e9, PEAK_HBM_GBPS, "GB/s"
+        return flops / (ms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s"
+
+    achieved, peak, roof_unit = roof(k_timed)
+    achieved_fl, _, _ = roof(k_flushed)
+
+    # Correctness of the timed configuration against an fp32 torch loop
+    # (every row up to 64 Mi output elements, else a row sample).
     c = step()
-    ref = gg.reference_grouped_gemm(case.a.float(), case.b.float(), offs)
-    max_abs = (c.float() - ref).abs().max().item()
+    if case.m * case.n <= 64 * 2 ** 20:
+        ref = gg.reference_grouped_gemm(case.a.float(), case.b.float(), offs)
+        max_abs = (c.float() - ref).abs().max().item()
+    else:
+        rows = torch.arange(0, case.m, 509, device=dev)
+        bounds = torch.cumsum(case.counts, 0).to(dev)
+        e_of = torch.searchsorted(bounds, rows, right=True)
+        ref = torch.bmm(case.a[rows].float().unsqueeze(1), case.b[e_of].float()).squeeze(1)
+        max_abs = (c[rows].float() - ref).abs().max().item()
     del ref
-    tolerance = 2e-2 * math.sqrt(case.k / 512)
+    tolerance = 2e-2 * math.sqrt(max(case.k, 512) / 512)
 
     extra = {}
     if not args.no_compare:
@@ -601,11 +719,14 @@ def main():
             legs[name] = {"kernel_ms_median": round(t, 5),
                           "tflops": round(flops / (t * 1e-3) / 1e12, 1)}
         extra["reference_calls"] = legs
+        progress("expert MLP leg")
         extra["expert_mlp"] = expert_mlp_summary(dev)
+        progress("fp8 leg")
         extra["fp8"] = fp8_summary(dev)
+        progress("schedules leg")
         sched = {}
         for wl in ("uniform", "skewed"):
-            cs = case if wl == args.workload else workloads.make_case(wl, device=dev)
+            cs = case if (wl == case.name and is_metric_config) else workloads.make_case(wl, device=dev)
             o = gg.expert_offsets_from_recv_counts(cs.counts, device=dev)
             for mode in ("striped", "atomic"):
                 fn = lambda: gg.persistent_grouped_gemm(
@@ -636,18 +757,19 @@ def main():
             tb = event_times_ms(bmm, 50)
             extra["hipblaslt_bmm_ms_median"] = round(median(tb), 4)
             extra["hipblaslt_bmm_tflops"] = round(flops / (median(tb) * 1e-3) / 1e12, 1)
+        progress("overlap leg")
         extra["overlap"] = overlap_summary(case, offs, dev)
-        # Cache-cold launches: a 512 MiB write evicts L2 and the 256 MB MALL.
-        scratch = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
-        cold = event_times_ms(step, 20, flush=lambda: scratch.fill_(1.0))
-        extra["cold_kernel_ms_median"] = round(median(cold), 4)
-        extra["cold_tflops"] = round(flops / (median(cold) * 1e-3) / 1e12, 1)
-        del scratch
+        progress("reference benchmark default problem leg")
+        extra["reference_bench_default"] = reference_bench_summary(dev, dtype, args.num_sms)
 
+    progress("cpu baseline")
     cpu = None if args.no_cpu_baseline else cpu_baseline(case, args.cpu_seconds)
 
+    metric = METRIC if is_metric_config else (
+        f"grouped GEMM TFLOP/s, E={case.num_experts} {int(case.counts.max())} tok/expert "
+        f"K{case.k} N{case.n} ({args.dtype})")
     result = {
-        "metric": METRIC,
+        "metric": metric,
         "value": round(value, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -657,7 +779,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": args.dtype,
         "data": ("synthetic (N(0,1) tokens, N(0,1/K) weights, random init)" if args.operands == "random"
                  else f"synthetic, operands {args.operands} (power analysis, not the metric)"),
         "config": {
@@ -681,20 +803,33 @@ def main():
         "clock": r["clock"],
         "max_abs_diff_vs_fp32": round(max_abs, 6),
         "tolerance": round(tolerance, 6),
+        "flushed": {
+            "kernel_ms_median": round(k_flushed, 5),
+            "kernel_ms_min": round(min(flushed), 5),
+            "launches": len(flushed),
+            "flush_bytes_per_launch": FLUSH_BYTES,
+            "tflops": round(flops / (k_flushed * 1e-3) / 1e12, 1),
+            "roofline_achieved": round(achieved_fl, 2),
+            "roofline_frac": round(achieved_fl / peak, 4),
+            "protocol": "a 512 MiB device write before each launch (L2 and MALL evicted), "
+                        "HIP events around the launch",
+        },
         "roofline": {
-            "bound": "mfma",
+            "bound": "hbm" if hbm_bound else "mfma",
             "achieved": round(achieved, 2),
-            "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "achieved_from": "HIP events around the timed steps (GPU time per launch)",
-            "traffic": recorded_traffic(args.mode, args.workload, kernel_tile),
+            "peak": peak,
+            "unit": roof_unit,
+            "frac": round(achieved / peak, 4),
+            "achieved_from": "HIP events around the timed steps (GPU time per launch), warm caches; "
+                             "the flushed field has the cache-cold fraction",
+            "traffic": recorded_traffic(args.mode, case.name, kernel_tile),
             "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), "
                               "profiles/grouped_gemm_256x256_bf16_uniform.md",
-            "kernel": KERNEL_NAME if kernel_tile == (256, 256) else "grouped_gemm_kernel",
+            "kernel": (KERNEL_NAME.replace("Bf16", "Bf16" if args.dtype == "bf16" else "F16")
+                       if kernel_tile == (256, 256) else "grouped_gemm_kernel"),
             "algorithmic_flops_per_launch": flops,
-            "algorithmic_bytes_per_launch": case.algorithmic_bytes(),
-            "hbm_gbps_at_algorithmic_bytes": round(case.algorithmic_bytes() / (k_timed * 1e-3) / 1e9, 1),
+            "algorithmic_bytes_per_launch": nbytes,
+            "hbm_gbps_at_algorithmic_bytes": round(nbytes / (k_timed * 1e-3) / 1e9, 1),
         },
         "cpu_baseline": cpu,
         **extra,

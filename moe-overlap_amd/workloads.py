@@ -181,6 +181,17 @@ def make_fp8_case(tokens: int = 4096, experts: int = 64, top_k: int = 6, k: int 
     return case
 
 
+# The reference benchmark script's default problem (src/bench_triton_grouped_gemm.py:11-17,
+# :36-42): 256 routed experts x 128 tokens each, hidden 7168, ffn 2048, uniform counts.
+REFERENCE_BENCH = dict(experts=256, tokens_per_expert=128, k=7168, n=2048)
+
+
+def uniform_case(experts: int, tokens_per_expert: int, k: int, n: int,
+                 name: str = "uniform_custom") -> GroupedGemmCase:
+    """Equal counts, as the reference benchmark's build_counts makes them (:36-42)."""
+    return GroupedGemmCase(name, torch.full((experts,), tokens_per_expert, dtype=torch.int32), k, n)
+
+
 def make_case(
     name: str,
     device: Optional[torch.device] = None,
@@ -188,8 +199,12 @@ def make_case(
     seed: int = 0,
     materialize: bool = True,
 ) -> GroupedGemmCase:
-    """One of: cpu_plumbing (fp32, E=8), uniform (E=16, 512 rows each), skewed (16384 rows)."""
-    if name == "cpu_plumbing":
+    """One of: cpu_plumbing (fp32, E=8), uniform (E=16, 512 rows each), skewed (16384 rows),
+    reference_bench (the reference benchmark script's default: E=256 x 128 rows, K=7168,
+    N=2048)."""
+    if name == "reference_bench":
+        case = uniform_case(name=name, **REFERENCE_BENCH)
+    elif name == "cpu_plumbing":
         case = GroupedGemmCase(name, torch.full((8,), 128, dtype=torch.int32), 512, 1024)
     elif name == "uniform":
         case = GroupedGemmCase(name, torch.full((16,), 512, dtype=torch.int32), 2048, 4096)
@@ -203,12 +218,14 @@ def make_case(
 
 
 def fill_operands(case: GroupedGemmCase, device=None, dtype=torch.bfloat16, seed: int = 0) -> None:
-    """a ~ N(0,1) [M, K], b ~ N(0, 1/K) [E, K, N], drawn in fp32 then cast."""
+    """a ~ N(0,1) [M, K], b ~ N(0, 1/K) [E, K, N], drawn in fp32 then cast (B one expert
+    at a time, so no fp32 copy of a large weight tensor is ever whole)."""
     device = torch.device("cpu") if device is None else torch.device(device)
     gen = torch.Generator(device=device).manual_seed(seed)
     a = torch.randn(case.m, case.k, generator=gen, device=device, dtype=torch.float32)
-    b = torch.randn(case.num_experts, case.k, case.n, generator=gen, device=device,
-                    dtype=torch.float32)
-    b.mul_(1.0 / math.sqrt(case.k))
     case.a = a.to(dtype)
-    case.b = b.to(dtype)
+    del a
+    case.b = torch.empty(case.num_experts, case.k, case.n, device=device, dtype=dtype)
+    for e in range(case.num_experts):
+        w = torch.randn(case.k, case.n, generator=gen, device=device, dtype=torch.float32)
+        case.b[e] = w.mul_(1.0 / math.sqrt(case.k))

@@ -80,9 +80,11 @@ def test_noalloc_layout_rejects_oversized_workspace(cuda_device):
     lib = nat.lib()
     # 300000 assignments over 1024 experts need 293 * 1024 * 4 bytes > 1 MiB.
     assert lib.mgg_dispatch_layout_workspace_bytes(300000, 1, 1024) > 1 << 20
-    fake = ctypes.c_void_p(1 << 20)
-    rc = lib.mgg_dispatch_layout_noalloc(fake, nat.MGG_INT64, 300000, 1, 1024, fake, fake, fake,
-                                         fake, fake, None)
+    # Null pointers: the size check must reject the call before any pointer
+    # is used (were it skipped, the null checks behind it would answer
+    # MGG_ERR_INVALID instead, still without a launch).
+    rc = lib.mgg_dispatch_layout_noalloc(None, nat.MGG_INT64, 300000, 1, 1024, None, None, None,
+                                         None, None, None)
     assert rc == nat.MGG_ERR_UNSUPPORTED
     assert b"1 MiB" in lib.mgg_last_error()
     # The largest layout that fits (256 chunks x 1024 experts = 1 MiB) is accepted.
