@@ -757,6 +757,24 @@ def main():
             tb = event_times_ms(bmm, 50)
             extra["hipblaslt_bmm_ms_median"] = round(median(tb), 4)
             extra["hipblaslt_bmm_tflops"] = round(flops / (median(tb) * 1e-3) / 1e12, 1)
+        # N not a multiple of 8 is read and written in place: N = 4092 against
+        # N = 4096 on the metric's other dimensions.
+        progress("odd-N leg")
+        odd = {}
+        for n_odd in (4096, 4092):
+            co = workloads.uniform_case(case.num_experts, int(case.counts[0]), case.k, n_odd)
+            workloads.fill_operands(co, device=dev, dtype=dtype)
+            oo = gg.expert_offsets_from_recv_counts(co.counts, device=dev)
+            fn = lambda: gg.persistent_grouped_gemm(co.a, co.b, oo, num_sms=args.num_sms,
+                                                    use_atomic_queue=atomic)
+            settle_clock(fn)
+            t = median(event_times_ms(fn, 50))
+            odd[f"n{n_odd}"] = {"kernel_ms_median": round(t, 5),
+                                "tflops": round(co.flops / (t * 1e-3) / 1e12, 1)}
+            del co, oo
+        odd["ratio_4092_over_4096"] = round(odd["n4092"]["kernel_ms_median"]
+                                            / odd["n4096"]["kernel_ms_median"], 4)
+        extra["n_not_multiple_of_8"] = odd
         progress("overlap leg")
         extra["overlap"] = overlap_summary(case, offs, dev)
         progress("reference benchmark default problem leg")

@@ -172,15 +172,19 @@ int mgg_build_work_queue_host(const int64_t* expert_offsets, int64_t num_experts
  * If the queue is empty, C is zero-filled; with K == 0 the covered rows are
  * zeros (A and B and their strides are not read).  Rows of C not covered by
  * any expert range are left unwritten.  Supported: dtype BF16/FP16,
- * block_m, block_n in {64, 128, 256}, N % 8 == 0, strides multiples of 8
- * elements, 16-byte aligned base pointers, E <= 2048 when the queue is
- * derived on the device.  K % 8 == 0 for K-major B; with N-major B any K:
+ * block_m, block_n in {64, 128, 256}, N even (B's and C's rows are read and
+ * written at any 4-byte alignment; the last chunk of a C row is stored by
+ * words), lda (and ldb_k of K-major B) a multiple of 8 elements, ldb_k of
+ * N-major B, ldb_e and ldc even, 16-byte aligned base pointers, E <= 2048
+ * when the queue is derived on the device.  K % 8 == 0 for K-major B; with
+ * N-major B any K:
  * B's rows at and past K are never read (they count as zeros), while A is
  * read up to the next multiple of 8, so lda must cover it and A's elements
  * in those columns must be finite (they are multiplied by zeros; the drop-in
  * makes them zeros).
  * (ABI version 4 added report_block_m, report_block_n; version 6 any K for
- * N-major B; version 7 the split controls and per-capture counter words.)
+ * N-major B; version 7 the split controls, per-capture counter words and
+ * any even N.)
  */
 int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
                      const int32_t* expert_offsets, int64_t m_size, int64_t k_size, int64_t n_size,
@@ -244,7 +248,7 @@ int mgg_grouped_gemm_gathered(int dtype, int epilogue, const void* a, const int3
  * Queue (derived on the device, or prebuilt), schedules, work_counter and
  * empty-queue behaviour as in mgg_grouped_gemm.  Tiles 256x256, 256x128,
  * 192x128 and 128x128; K, lda, ldb_n, ldb_e multiples of 16; N, ldc
- * multiples of 8.
+ * even.
  * (Introduced with ABI version 2; version 4 added the queue and report-tile
  * arguments.)
  */

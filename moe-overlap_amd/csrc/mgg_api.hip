@@ -484,7 +484,12 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   if (m_size < 0 || k_size < 0 || n_size < 0 || num_experts < 0)
     return set_error(MGG_ERR_INVALID, "sizes must be >= 0");
   if (m_size == 0 || n_size == 0) return MGG_OK;  // C has no elements
-  if (n_size % 8 != 0) return set_error(MGG_ERR_UNSUPPORTED, "K and N must be multiples of 8");
+  // N even: B's and C's rows need not be 16-byte aligned (16-byte DMAs and
+  // stores run at any 2-byte alignment); the last chunk of a row is read as
+  // it lies and stored by words.  (With N odd the word holding B's last
+  // element would straddle the end of its buffer descriptor, where the range
+  // check zeroes the whole word.)
+  if (n_size % 2 != 0) return set_error(MGG_ERR_UNSUPPORTED, "N must be even");
   // K not a multiple of 8 (16-bit N-major B only): A is read to the next
   // multiple of 8 (those columns meet B rows that read as zeros), B's rows
   // stop at K.
@@ -509,8 +514,10 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   if (report_block_n <= 0) report_block_n = block_n;
   if (lda < k_a || ldb_k < (b_rows_k ? k_size : n_size) || ldc < c_cols || ldb_e < 0)
     return set_error(MGG_ERR_INVALID, "leading dimensions smaller than the matrix extents");
-  if (lda % 8 != 0 || ldb_k % 8 != 0 || ldb_e % 8 != 0 || ldc % 8 != 0)
-    return set_error(MGG_ERR_UNSUPPORTED, "strides must be multiples of 8 elements");
+  if (lda % 8 != 0 || ldb_k % (b_rows_k ? 8 : 2) != 0 || ldb_e % 2 != 0 || ldc % 2 != 0)
+    return set_error(MGG_ERR_UNSUPPORTED,
+                     "strides must be multiples of 8 elements (lda; ldb_k of K-major B) or of 2 "
+                     "(ldb_k of N-major B, ldb_e, ldc)");
   // A and B may be null only when nothing reads them (no experts or K == 0).
   const bool reads_ab = num_experts > 0 && k_size > 0;
   if (c == nullptr || expert_offsets == nullptr || (reads_ab && (a == nullptr || b == nullptr)))

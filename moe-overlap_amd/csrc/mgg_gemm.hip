@@ -295,16 +295,23 @@ __device__ __forceinline__ int32_t ticket_from(unsigned long long raw, unsigned 
   return first_ticket(word, epoch);
 }
 
-// Cooperative zero fill of C[M, cols] (the empty-queue case, :369-371).
+// Cooperative zero fill of C[M, cols] (the empty-queue case, :369-371): 8
+// columns per lane, the last chunk of a row (cols even, not a multiple of 8)
+// by words.
 __device__ void zero_fill(const GemmParams& p, int64_t cols) {
-  const int64_t chunks_per_row = cols / 8;
+  const int64_t chunks_per_row = (cols + 7) / 8;
   const int64_t total = p.m * chunks_per_row;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const u32x4 z = {0u, 0u, 0u, 0u};
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
     const int64_t r = i / chunks_per_row;
     const int64_t c8 = i - r * chunks_per_row;
-    *reinterpret_cast<u32x4*>(p.c + r * p.ldc + c8 * 8) = z;
+    uint16_t* dst = p.c + r * p.ldc + c8 * 8;
+    if (c8 * 8 + 8 <= cols) {
+      *reinterpret_cast<u32x4*>(dst) = z;
+    } else {
+      for (int64_t w = 0; c8 * 8 + 2 * w < cols; ++w) reinterpret_cast<uint32_t*>(dst)[w] = 0u;
+    }
   }
 }
 
@@ -648,9 +655,15 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       for (int t = 0; t < kBPerWave; ++t) {
         const int k = b_krow(t);
         const int swz = BN >= 128 ? 4 * (k & 3) : 4 * ((k >> 1) & 1);
-        int64_t col = 8 * ((lane % kBChunks) ^ swz);
-        col = c.n0 + col > p.n - 8 ? p.n - 8 - c.n0 : col;
-        b_voff[t] = (uint32_t)((k * p.ldb_k + col) * 2);
+        const int64_t col = 8 * ((lane % kBChunks) ^ swz);
+        // A chunk wholly past N reads the row's last 8 columns instead
+        // (its outputs are never stored; N < 8: zeros); the chunk that holds
+        // column N-1 (N not a multiple of 8) is read as it lies, its columns
+        // past N coming from the next row, or as zeros past the descriptor.
+        if (c.n0 + col < p.n)
+          b_voff[t] = (uint32_t)((k * p.ldb_k + col) * 2);
+        else
+          b_voff[t] = p.n >= 8 ? (uint32_t)((k * p.ldb_k + p.n - 8 - c.n0) * 2) : kOutOfRange;
       }
     }
   };
@@ -1093,11 +1106,24 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     const auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
     return u32x4{(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
   };
+  // 8 consecutive outputs at crow + col, of which those before column
+  // `cols` are stored: one 16-byte store, or (the last chunk of a row when
+  // the row length is not a multiple of 8; it is even, so whole words) one
+  // store per pair.
+  auto store_chunk = [&](uint16_t* crow, int64_t col, int64_t cols, const u32x4& v) {
+    if (col + 8 <= cols) {
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(crow + col));
+    } else if (col < cols) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        if (col + 2 * w < cols) __builtin_nontemporal_store(v[w], reinterpret_cast<uint32_t*>(crow + col) + w);
+    }
+  };
   auto store_pair = [&](uint16_t* crow, int64_t col, int64_t cols, bool row_ok,
                         const float* y0, const float* y1) {
     const u32x4 v = pack_pair(y0, y1);
     // col already includes 8*half
-    if (row_ok && col < cols) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(crow + col));
+    if (row_ok) store_chunk(crow, col, cols, v);
   };
   // Stores through LDS: a wave's output columns of a row are one 64- or
   // 128-byte segment of C, but a store instruction straight from the MFMA
@@ -1159,8 +1185,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
           *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(lds_ptr(lds) + line_addr(rr, ch));
       const int mr = wm * (BM / 2) + 32 * j + rr;
       const int64_t gr = c.row_base + mr;
-      if (mr < c.rows_valid && gr >= 0 && gr <= last_row && col < cols)
-        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p.c + gr * p.ldc + col));
+      if (mr < c.rows_valid && gr >= 0 && gr <= last_row) store_chunk(p.c + gr * p.ldc, col, cols, v);
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();

@@ -44,11 +44,12 @@ Differences, all in arguments that do not change results:
   The parts meet in a per-stream workspace of 64 MiB (one 256 x 256 fp32
   slot per CU) that the stream's first atomic call allocates, unless
   ``reserve_split_workspace`` made it beforehand.
-* Operands whose inner stride is not 1 or whose rows are not 16-byte aligned
-  are copied on the device first.  K not a multiple of 8: A is copied with
+* Operands whose inner stride is not 1 are copied on the device first, and
+  so is A when its row stride is not a multiple of 8 elements.  K not a multiple of 8: A is copied with
   zero columns to the next multiple of 8 and B is read in place (the kernel
-  stops B's rows at K; a K-major B view is copied).  N not a multiple of 8: B
-  is copied zero-padded and C sliced.  K == 0 gives zeros, as there.
+  stops B's rows at K; a K-major B view is copied).  Any even N is read and
+  written in place (B's and C's rows need not be 16-byte aligned); odd N: B
+  is copied with one zero column and C sliced.  K == 0 gives zeros, as there.
 """
 from __future__ import annotations
 
@@ -278,11 +279,13 @@ def _requested_tile(block_m, block_n) -> Tuple[int, int]:
     return out[0], out[1]
 
 
-def _fast_layout(t: torch.Tensor) -> bool:
-    """Unit inner stride, 16-byte aligned base, outer strides multiples of 8."""
+def _fast_layout(t: torch.Tensor, mult: int = 8) -> bool:
+    """Unit inner stride, 16-byte aligned base, outer strides multiples of
+    `mult` elements (8 for A; 2 for N-major B, whose rows the kernel reads at
+    any 4-byte alignment)."""
     if t.stride(-1) != 1 or t.data_ptr() % 16 != 0:
         return False
-    return all(t.stride(d) % 8 == 0 for d in range(t.dim() - 1) if t.size(d) > 1)
+    return all(t.stride(d) % mult == 0 for d in range(t.dim() - 1) if t.size(d) > 1)
 
 
 def _kmajor_layout(b: torch.Tensor) -> bool:
@@ -297,12 +300,12 @@ def _kmajor_layout(b: torch.Tensor) -> bool:
     return b.size(0) < 2 or b.stride(0) % 8 == 0
 
 
-def _gemm_operand(t: torch.Tensor) -> torch.Tensor:
+def _gemm_operand(t: torch.Tensor, mult: int = 8) -> torch.Tensor:
     """`t` itself when the kernel can read it in place, else a device copy."""
-    if _fast_layout(t):
+    if _fast_layout(t, mult):
         return t
     t = t.contiguous()
-    if not _fast_layout(t):
+    if not _fast_layout(t, mult):
         t = t.clone(memory_format=torch.contiguous_format)
     return t
 
@@ -389,10 +392,12 @@ def persistent_grouped_gemm(
 
     # K not a multiple of 8: A is zero-padded on the device to the next
     # multiple of 8 and B is read as it lies (the kernel stops B's rows at K,
-    # so the padding columns meet zeros).  N not a multiple of 8: B is
-    # zero-padded and C sliced.
+    # so the padding columns meet zeros).  Even N: B and C are used as they
+    # lie (the kernel reads and writes rows at any 4-byte alignment).  Odd N:
+    # B is zero-padded by one column and C sliced (the word holding B's last
+    # element would straddle the end of the kernel's buffer descriptor).
     k_pad = (k_size + 7) // 8 * 8
-    n_pad = (n_size + 7) // 8 * 8
+    n_pad = n_size + (n_size & 1)
     a_op, b_op = a_cat, b_expert
     # B stored [E, N, K] is read as it lies (no transposing copy).
     b_kmajor = k_pad == k_size and n_pad == n_size and _kmajor_layout(b_expert)
@@ -403,7 +408,7 @@ def persistent_grouped_gemm(
     if k_pad > 0:
         a_op = _gemm_operand(a_op)
         if not b_kmajor:
-            b_op = _gemm_operand(b_op)
+            b_op = _gemm_operand(b_op, 2)
     # Leading dimensions; a size-1 dimension's stride is never used, nor are
     # A's and B's when K == 0.  ldb_k is the stride between B's rows: K rows,
     # or N rows for K-major B.
@@ -520,9 +525,9 @@ def _persistent_grouped_gemm_fp8(a_cat, b_expert, expert_offsets, a_scale, b_sca
     if int(num_sms) <= 0:
         raise ValueError("num_sms must be positive.")
     counter_dev = _counter_arg(work_counter, use_atomic_queue, device)
-    # K to a multiple of 16, N to a multiple of 8 (zero padding adds nothing).
+    # K to a multiple of 16, N to an even count (zero padding adds nothing).
     k_pad = (k_size + 15) // 16 * 16
-    n_pad = (n_size + 7) // 8 * 8
+    n_pad = n_size + (n_size & 1)
     a_op = a_cat
     if k_pad != k_size:
         a_op = torch.nn.functional.pad(a_op.view(torch.uint8), (0, k_pad - k_size)).view(a_cat.dtype)

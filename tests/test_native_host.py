@@ -105,9 +105,13 @@ def gemm_call(**over):
     (dict(dtype=nat.MGG_DTYPE_BF16 | nat.MGG_B_KMAJOR, k=60, lda=64, ldb_k=64, ldb_e=64 * 64),
      nat.MGG_ERR_UNSUPPORTED, b"multiples of 8"),
     (dict(k=60, lda=56), nat.MGG_ERR_INVALID, b"leading"),
-    (dict(n=60), nat.MGG_ERR_UNSUPPORTED, b"multiples of 8"),
+    # N even is read in place (n=60 passes this check); odd N is not.
+    (dict(n=61, ldb_k=64, ldc=64), nat.MGG_ERR_UNSUPPORTED, b"N must be even"),
     (dict(lda=32), nat.MGG_ERR_INVALID, b"leading"),
-    (dict(ldb_k=72, ldb_e=60), nat.MGG_ERR_UNSUPPORTED, b"strides"),
+    (dict(ldb_k=72, ldb_e=61), nat.MGG_ERR_UNSUPPORTED, b"strides"),
+    (dict(ldb_k=65), nat.MGG_ERR_UNSUPPORTED, b"strides"),
+    (dict(lda=68), nat.MGG_ERR_UNSUPPORTED, b"strides"),
+    (dict(ldc=66, n=60, ldb_k=60, ldb_e=60 * 64, a=FAKE + 8), nat.MGG_ERR_UNSUPPORTED, b"aligned"),
     (dict(a=None), nat.MGG_ERR_INVALID, b"null"),
     (dict(off=None), nat.MGG_ERR_INVALID, b"null"),
     (dict(a=FAKE + 8), nat.MGG_ERR_UNSUPPORTED, b"aligned"),
