@@ -49,9 +49,9 @@
 #ifndef MGG_FP8_NW
 #define MGG_FP8_NW 8
 #endif
-// Most parts a tile of a short last round is split into: 1 << MGG_SPLIT_MAX_LOG.
-#ifndef MGG_SPLIT_MAX_LOG
-#define MGG_SPLIT_MAX_LOG 2
+// Most parts a tile of a short last round is split into.
+#ifndef MGG_SPLIT_MAX
+#define MGG_SPLIT_MAX 4
 #endif
 
 namespace mgg {
@@ -463,29 +463,29 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   const int G = gridDim.x;
   const int64_t K = p.k;
   // ---- split last round (atomic schedule, device-derived queue) ----------
-  // When the tiles past the last full round of G are at most G/s for s = 4
-  // or 2 (and the library provided the partial-sum workspace), each of them
-  // becomes s work items, the parts q = 0 .. s-1 of K, [K_q, K_q+1) with
-  // K_q = floor(q * n_gran / s) granules, taken by s workers: the last round
-  // runs on s times as many CUs for 1/s as long.  Queue items past w_base
-  // are the parts (item w_base + s*t + q is part q of tile w_base + t); W
-  // counts work items.  The parts meet pairwise in split_fixup.  A granule
-  // is an A block (A-block tile) or a stage, so every part starts on a stage
-  // boundary; each part holds at least two.  The striped schedule keeps
-  // whole tiles.
+  // When the rem tiles past the last full round of G are at most G/s for
+  // some s in 2 .. MGG_SPLIT_MAX (the largest such s is taken; the library
+  // provided the partial-sum workspace), each of them becomes s work items,
+  // the parts q = 0 .. s-1 of K, [K_q, K_q+1) with K_q = floor(q * n_gran /
+  // s) granules, taken by s workers: the last round runs on s times as many
+  // CUs for 1/s as long.  Queue items past w_base are the parts (item w_base
+  // + s*t + q is part q of tile w_base + t); W counts work items.  The parts
+  // meet pairwise in split_fixup.  A granule is an A block (A-block tile) or
+  // a stage, so every part starts on a stage boundary; each part holds at
+  // least two.  The striped schedule keeps whole tiles.
   constexpr int kGran = kABlk ? 2 * kBK : kBK;
   const int n_gran = (int)((K + kGran - 1) / kGran);
   int32_t w_base = W_tiles;
   int32_t W = W_tiles;
-  int split_log = 0;  // s = 1 << split_log parts per split tile
+  int split_s = 1;  // parts per split tile
   if (p.atomic && p.num_work < 0 && p.split_flags != nullptr) {
     const int32_t rem = W_tiles > G ? W_tiles % G : W_tiles;
-    for (int l = MGG_SPLIT_MAX_LOG; l >= 1 && split_log == 0; --l)
-      if (rem > 0 && (rem << l) <= G && (rem << l) <= p.split_slots && n_gran >= (2 << l))
-        split_log = l;
-    if (split_log > 0) {
+    for (int sp = MGG_SPLIT_MAX; sp >= 2 && split_s == 1; --sp)
+      if (rem > 0 && (int64_t)rem * sp <= G && (int64_t)rem * sp <= p.split_slots && n_gran >= 2 * sp)
+        split_s = sp;
+    if (split_s > 1) {
       w_base = W_tiles - rem;
-      W = w_base + (rem << split_log);
+      W = w_base + rem * split_s;
     }
   }
   // Atomic schedule: tickets 0 .. W-1 are drawn in all.  Items past the
@@ -532,7 +532,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     c.slot = -1;
     if (item >= w_base) {  // a part of a split tile
       c.slot = item - w_base;
-      item = w_base + (c.slot >> split_log);
+      item = w_base + c.slot / split_s;
     }
     int e, tm, tn;
     if (p.num_work >= 0) {
@@ -623,9 +623,9 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     // ke, so every stage offset below is relative to kb.
     int kb = 0, klen = (int)K;
     if (c.slot >= 0) {
-      const int q = c.slot & ((1 << split_log) - 1);
-      kb = ((q * n_gran) >> split_log) * kGran;
-      const int ke = q == (1 << split_log) - 1 ? (int)K : (((q + 1) * n_gran) >> split_log) * kGran;
+      const int q = c.slot % split_s;
+      kb = (q * n_gran / split_s) * kGran;
+      const int ke = q == split_s - 1 ? (int)K : ((q + 1) * n_gran / split_s) * kGran;
       klen = ke - kb;
     }
     k_size = klen;
@@ -1302,27 +1302,35 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   };
   static_assert(kQuads * 1024 * NW == BM * BN * 4, "a partial slot is the tile's fp32 sums");
   // The s parts of a split tile meet in a binary tree of s - 1 meetings.  At
-  // level l a worker holds the sum of the 2^l parts from b = q & -2^l (its
-  // accumulators), and meets the holder of the sibling subtree b ^ 2^l on
-  // the level's flag word for the pair.  It either finds the sibling
-  // finished (the flag reads count 1 in this launch's epoch) or writes its
-  // sums to slot s*t + b, waits until they are complete, and takes a ticket
-  // on the flag (the dequeue's epoch-tagged claim, so a flag left by an
-  // unfinished launch reads as fresh).  The worker that finds the sibling
-  // finished, or draws ticket 1, returns the flag to 0, adds the sibling's
-  // sums from slot s*t + (b ^ 2^l) and goes on to the next level; the other
-  // is done.  The worker that completes the last level stores the tile
-  // (returns true).  fp32 addition is commutative, so every meeting's sum,
-  // and the tile, is the same whichever worker arrives first, and no worker
-  // ever waits for another.  Flag words of tile t: s*t + (s - (s >> l)) +
-  // (q >> (l + 1)) at level l.
+  // level l a worker holds the sum of the parts [b, min(b + 2^l, s)) with
+  // b = q & -2^l (its accumulators); when the sibling subtree, from
+  // b ^ 2^l, exists (b ^ 2^l < s), the two holders meet on the level's flag
+  // word for the pair, else the worker goes on to the next level alone.  At
+  // a meeting a worker either finds the sibling finished (the flag reads
+  // count 1 in this launch's epoch) or writes its sums to slot s*t + b,
+  // waits until they are complete, and takes a ticket on the flag (the
+  // dequeue's epoch-tagged claim, so a flag left by an unfinished launch
+  // reads as fresh).  The worker that finds the sibling finished, or draws
+  // ticket 1, returns the flag to 0, adds the sibling's sums from slot s*t +
+  // (b ^ 2^l) and goes on to the next level; the other is done.  The worker
+  // that completes the last level stores the tile (returns true).  fp32
+  // addition is commutative, so every meeting's sum, and the tile, is the
+  // same whichever worker arrives first, and no worker ever waits for
+  // another.  Tile t's s - 1 flag words start at (s - 1) * t: level l's
+  // pairs follow those of the levels below it, pair q >> (l + 1) of the
+  // ceil(s / 2^l) subtrees at that level.
   auto split_fixup = [&](const Coords& c) -> bool {
-    const int s = 1 << split_log;
-    const int32_t t = c.slot >> split_log;
-    const int q = c.slot & (s - 1);
-    for (int l = 0; l < split_log; ++l) {
-      unsigned long long* flag = p.split_flags + (int64_t)s * t + (s - (s >> l)) + (q >> (l + 1));
+    const int s = split_s;
+    const int32_t t = c.slot / s;
+    const int q = c.slot - t * s;
+    int64_t level_flags = (int64_t)(s - 1) * t;  // first flag word of level l
+    int subtrees = s;                              // ceil(s / 2^l)
+    for (int l = 0; (1 << l) < s; ++l) {
       const int32_t b = q & -(1 << l);
+      unsigned long long* flag = p.split_flags + level_flags + (q >> (l + 1));
+      level_flags += subtrees >> 1;
+      subtrees = (subtrees + 1) >> 1;
+      if ((b ^ (1 << l)) >= s) continue;  // no sibling subtree at this level
       if (tid == 0) {
         const unsigned long long f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_item[1] = ((uint32_t)(f >> 32) == p.epoch && (uint32_t)f == 1u) ? 1 : 0;

@@ -52,7 +52,7 @@ def explicit(xg, w, offs, epi, out_cols, workers, atomic):
 # (counts, T source rows, K, N, workers; 0 = the CU count): ragged experts
 # with an empty one, a one-row expert and a partial K stage.  Atomic launches
 # split their last round: case 0 its 16 tiles in 4 parts, case 1 (7 workers)
-# the 2 tiles past two rounds in halves, case 2 (K = 264) its 5 tiles in
+# the 2 tiles past two rounds in thirds, case 2 (K = 264) its 5 tiles in
 # halves, case 3 its 64 tiles in 4 parts.
 CASES = [([300, 0, 257, 1, 600], 700, 1032, 512, 0),
          ([300, 0, 257, 1, 600], 700, 1032, 512, 7),

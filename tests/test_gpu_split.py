@@ -55,11 +55,11 @@ def tiles(counts, n, bm, bn):
 
 def split_parts(w, g, k, gran=64):
     """(tiles split, parts per tile) of the atomic schedule's last round: the
-    most parts s in (4, 2) with s * rem <= g and at least two K granules
+    most parts s in (4, 3, 2) with s * rem <= g and at least two K granules
     (64-deep A blocks of the 256x256 tile) per part."""
     rem = w % g if w > g else w
     n_gran = -(-k // gran)
-    for s in (4, 2):
+    for s in (4, 3, 2):
         if 0 < rem and s * rem <= g and n_gran >= 2 * s:
             return rem, s
     return 0, 1
@@ -68,14 +68,18 @@ def split_parts(w, g, k, gran=64):
 # (counts, K, N, workers): 24 tiles of 256x256 on 256 workers (all split in
 # 4), on 20 (4 tiles past the full round, in 4), 7 (3 tiles in 2), 30 (24 >
 # 15: whole); K = 264: 3 tiles in halves of 128 and 136 (a partial stage);
-# K = 520: 3 tiles in quarters of 128, 128, 128 and 136.
+# K = 520: 3 tiles in quarters of 128, 128, 128 and 136; 28 tiles on 12
+# workers: the 4 past two rounds in thirds (3 * 4 <= 12 < 4 * 4), of K = 520
+# (128, 128, 264) and K = 400 (128, 128, 144).
 CASES = [([300, 0, 257, 1, 600], 1032, 520, 256),
          ([300, 0, 257, 1, 600], 1032, 520, 20),
          ([300, 0, 257, 1, 600], 1032, 520, 7),
          ([300, 0, 257, 1, 600], 1032, 520, 30),
          ([64] * 3, 264, 256, 256),
-         ([64] * 3, 520, 256, 256)]
-EXPECT_PARTS = [4, 4, 2, 1, 2, 4]
+         ([64] * 3, 520, 256, 256),
+         ([256] * 27 + [5], 520, 256, 12),
+         ([256] * 27 + [5], 400, 256, 12)]
+EXPECT_PARTS = [4, 4, 2, 1, 2, 4, 3, 3]
 
 
 @pytest.mark.parametrize("case", range(len(CASES)))
