@@ -203,6 +203,7 @@ def clock_pass(fn, launches=50):
 
 PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_256x256_bf16_uniform.md"
 FP8_PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_fp8_cfg5.md"
+REFBENCH_PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_256x256_bf16_reference_bench.md"
 
 
 def recorded_traffic(mode, workload, kernel_tile):
@@ -210,6 +211,8 @@ def recorded_traffic(mode, workload, kernel_tile):
     (calibrated against a plain copy), when one covers this configuration; else None."""
     if workload == "uniform" and kernel_tile == (256, 256):
         path, key = PROFILE_SUMMARY, f"traffic_bytes_per_launch_{mode}:"
+    elif workload == "reference_bench" and kernel_tile == (256, 256):
+        path, key = REFBENCH_PROFILE_SUMMARY, f"traffic_bytes_per_launch_reference_bench_{mode}:"
     elif workload == "fp8" and kernel_tile in ((256, 256), (256, 128), (192, 128)):
         path, key = FP8_PROFILE_SUMMARY, f"traffic_bytes_per_launch_fp8_{kernel_tile[0]}x{kernel_tile[1]}_{mode}:"
     else:
@@ -842,7 +845,9 @@ def main():
                              "the flushed field has the cache-cold fraction",
             "traffic": recorded_traffic(args.mode, case.name, kernel_tile),
             "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), "
-                              "profiles/grouped_gemm_256x256_bf16_uniform.md",
+                              + ("profiles/grouped_gemm_256x256_bf16_reference_bench.md"
+                                 if case.name == "reference_bench"
+                                 else "profiles/grouped_gemm_256x256_bf16_uniform.md"),
             "kernel": (KERNEL_NAME.replace("Bf16", "Bf16" if args.dtype == "bf16" else "F16")
                        if kernel_tile == (256, 256) else "grouped_gemm_kernel"),
             "algorithmic_flops_per_launch": flops,

@@ -957,7 +957,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // A block and B.
   constexpr int kWaitEven = kLB == 3 ? kBPerWave + kAPerWave + kBPerWave
                                      : kBPerWave + kBPerWave + kAPerWave + kBPerWave;
-  static_assert(!kABlk || (kAPerWave == 4 && kBPerWave == 2), "A-block DMA shares assume 4 + 2");
+  static_assert(!kABlk || (kAPerWave % 2 == 0 && kBPerWave % 2 == 0), "A-block DMA shares come in halves");
   auto issue_ablock = [&](int m, int t0, int t1) {  // DMAs [t0, t1) of A block m
     const int k0 = m * 2 * kBK;
     const uint32_t la = lds_a0 + (m & 1) * kASlot + wave * kAPerWave * 1024;
@@ -1009,10 +1009,10 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       mfma_group(0, g);
       if (g < 2) read_kstep_ab(H, 1, kt, 1, g);
       if constexpr (h == 0) {
-        if (g < 2) issue_ablock(kt / 2 + 1, 2 * g, 2 * g + 2);
-        else issue_bstage(kt + kLB, g - 2, g - 1);
+        if (g < 2) issue_ablock(kt / 2 + 1, g * kAPerWave / 2, (g + 1) * kAPerWave / 2);
+        else issue_bstage(kt + kLB, (g - 2) * kBPerWave / 2, (g - 1) * kBPerWave / 2);
       } else {
-        if (g == 0 || g == 2) issue_bstage(kt + kLB, g / 2, g / 2 + 1);
+        if (g == 0 || g == 2) issue_bstage(kt + kLB, g / 2 * kBPerWave / 2, (g / 2 + 1) * kBPerWave / 2);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
