@@ -56,7 +56,17 @@ METRIC = "grouped GEMM TFLOP/s + % bf16 MFMA peak, E=16 512 tok/expert K2048 N40
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0
 PEAK_FP8_TFLOPS = 5033.2  # MI355X dense fp8 MFMA
-KERNEL_NAME = "grouped_gemm_kernel<256,256,32,4,8,Bf16,0>"
+# (K per stage, LDS stages, waves) of the compiled 16-bit tiles bench.py names.
+_TILE_CONFIG = {(256, 256): (32, 4, 8), (128, 512): (32, 3, 8), (128, 128): (64, 4, 4)}
+
+
+def kernel_name(tile, dtype="bf16"):
+    """The rocprofv3 name of the 16-bit kernel instance for `tile`."""
+    cfg = _TILE_CONFIG.get(tuple(tile))
+    if cfg is None:
+        return "grouped_gemm_kernel"
+    t = "Bf16" if dtype == "bf16" else "F16"
+    return f"grouped_gemm_kernel<{tile[0]},{tile[1]},{cfg[0]},{cfg[1]},{cfg[2]},{t},0>"
 
 
 def parse_args():
@@ -203,7 +213,7 @@ def clock_pass(fn, launches=50):
 
 PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_256x256_bf16_uniform.md"
 FP8_PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_fp8_cfg5.md"
-REFBENCH_PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_256x256_bf16_reference_bench.md"
+REFBENCH_PROFILE_SUMMARY = REPO / "profiles" / "grouped_gemm_128x512_bf16_reference_bench.md"
 
 
 def recorded_traffic(mode, workload, kernel_tile):
@@ -211,7 +221,7 @@ def recorded_traffic(mode, workload, kernel_tile):
     (calibrated against a plain copy), when one covers this configuration; else None."""
     if workload == "uniform" and kernel_tile == (256, 256):
         path, key = PROFILE_SUMMARY, f"traffic_bytes_per_launch_{mode}:"
-    elif workload == "reference_bench" and kernel_tile == (256, 256):
+    elif workload == "reference_bench" and kernel_tile == (128, 512):
         path, key = REFBENCH_PROFILE_SUMMARY, f"traffic_bytes_per_launch_reference_bench_{mode}:"
     elif workload == "fp8" and kernel_tile in ((256, 256), (256, 128), (192, 128)):
         path, key = FP8_PROFILE_SUMMARY, f"traffic_bytes_per_launch_fp8_{kernel_tile[0]}x{kernel_tile[1]}_{mode}:"
@@ -655,7 +665,8 @@ def main():
         case.b.fill_(1.0 / 64)
     offs = gg.expert_offsets_from_recv_counts(case.counts, device=dev)
     atomic = args.mode == "atomic"
-    kernel_tile = _kernel_tile_arg(args.kernel_tile) or gg._default_kernel_tile(case.m, case.num_experts)
+    kernel_tile = (_kernel_tile_arg(args.kernel_tile)
+                   or gg._default_kernel_tile(case.m, case.num_experts, case.n))
     kw = dict(num_sms=args.num_sms, block_m=args.block_m, block_n=args.block_n,
               use_atomic_queue=atomic, kernel_tile=kernel_tile)
 
@@ -845,11 +856,10 @@ def main():
                              "the flushed field has the cache-cold fraction",
             "traffic": recorded_traffic(args.mode, case.name, kernel_tile),
             "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), "
-                              + ("profiles/grouped_gemm_256x256_bf16_reference_bench.md"
+                              + ("profiles/grouped_gemm_128x512_bf16_reference_bench.md"
                                  if case.name == "reference_bench"
                                  else "profiles/grouped_gemm_256x256_bf16_uniform.md"),
-            "kernel": (KERNEL_NAME.replace("Bf16", "Bf16" if args.dtype == "bf16" else "F16")
-                       if kernel_tile == (256, 256) else "grouped_gemm_kernel"),
+            "kernel": kernel_name(kernel_tile, args.dtype),
             "algorithmic_flops_per_launch": flops,
             "algorithmic_bytes_per_launch": nbytes,
             "hbm_gbps_at_algorithmic_bytes": round(nbytes / (k_timed * 1e-3) / 1e9, 1),

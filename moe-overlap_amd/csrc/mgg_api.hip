@@ -475,8 +475,9 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
     return set_error(MGG_ERR_UNSUPPORTED, "fp8 tiles are 256x256, 256x128, 192x128 and 128x128");
   if (epilogue != MGG_EPI_NONE && epilogue != MGG_EPI_GELU && epilogue != MGG_EPI_SWIGLU)
     return set_error(MGG_ERR_INVALID, "epilogue must be MGG_EPI_NONE, MGG_EPI_GELU or MGG_EPI_SWIGLU");
-  const bool block_ok = (block_m == 64 || block_m == 128 || block_m == 256) &&
-                        (block_n == 64 || block_n == 128 || block_n == 256);
+  const bool block_ok = ((block_m == 64 || block_m == 128 || block_m == 256) &&
+                         (block_n == 64 || block_n == 128 || block_n == 256)) ||
+                        (block_m == 128 && block_n == 512);
   if (!fp8 && !block_ok)  // fp8 tiles were checked above
     return set_error(MGG_ERR_UNSUPPORTED, "block_m/block_n must each be one of 64, 128, 256");
   if (!epilogue_supported(epilogue, block_m, block_n))

@@ -1557,6 +1557,7 @@ int launch_typed(int block_m, int block_n, const GemmParams& p, int workers, hip
     MGG_CASE(64, 64, 64, 4, 4)
     MGG_CASE(256, 64, 64, 3, 4)
     MGG_CASE(64, 256, 64, 3, 4)
+    MGG_CASE(128, 512, 32, 3, 8)
   }
 #undef MGG_CASE
   return set_error(MGG_ERR_UNSUPPORTED, EPI == kEpiNone

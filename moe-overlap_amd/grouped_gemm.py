@@ -76,7 +76,7 @@ __all__ = [
 
 # Tiles compiled into libmgg for bf16/fp16 (fused epilogues: 256x256, 128x128).
 _KERNEL_TILES = ((256, 256), (128, 128), (256, 128), (128, 256), (128, 64), (64, 128),
-                 (64, 64), (256, 64), (64, 256))
+                 (64, 64), (256, 64), (64, 256), (128, 512))
 _DTYPE_CODES = {torch.bfloat16: _nat.MGG_DTYPE_BF16, torch.float16: _nat.MGG_DTYPE_FP16}
 
 _WORK_QUEUE_CACHE: dict = {}
@@ -250,16 +250,26 @@ def _build_work_queue(
 # --------------------------------------------------------------------------
 # grouped GEMM
 # --------------------------------------------------------------------------
-def _default_kernel_tile(m_total: int, num_experts: int) -> Tuple[int, int]:
-    """256x256 for every expert size.  Rows of a tile past its expert's end are
+def _default_kernel_tile(m_total: int, num_experts: int, n_size: int = 4096) -> Tuple[int, int]:
+    """128x512 when the experts hold at most 128 rows on average and N is at
+    least 512, else 256x256.  Rows of a tile past its expert's end are
     zero-fill DMAs that read nothing, so a tile's cost follows the memory
-    requests of its valid rows, and the 256x256 kernel (two waves per SIMD)
-    makes the fewest per FLOP.  Measured on MI355X, E=16, K=2048, N=4096,
-    HIP-event medians (atomic / striped, µs): 64 rows per expert 57.2 / 52.3
-    against 128x256 63.4 / 54.5 and 128x128 55.4 / 50.9; 128 rows 60.9 / 60.5
-    against 95.5 / 94.6 (128x256); 192 rows 63.2 / 62.4 against 101.2 / 98.5;
-    256-384 rows 101-119 against 140-192."""
-    del m_total, num_experts
+    requests of its valid rows; both tiles hold the same 256 KiB of fp32
+    accumulators (two waves per SIMD).  With up to 128 rows an expert is one
+    m-tile either way, and the wide tile reads its A rows half as often.
+    Measured on MI355X (HIP-event medians, atomic / striped, µs): E=256 x 128
+    rows, K=7168, N=2048 (the reference benchmark's default problem) 1349 /
+    1332 against 1629 / 1633 (256x256); E=64 x 128, K=N=4096 417 / 404
+    against 472 / 467; E=128 x 64, K=7168, N=2048 626 / 615 against 753 /
+    745; but E=16 x 512, K=2048, N=4096 199 / 188 against 126 / 121 and E=32 x
+    256 205 / 180 against 135 / 133.  Among the tiles of at most 256 rows and
+    columns, 256x256 is the fastest at every expert size (E=16, K=2048,
+    N=4096: 64 rows per expert 57.2 / 52.3 against 128x256 63.4 / 54.5 and
+    128x128 55.4 / 50.9; 128 rows 60.9 / 60.5 against 95.5 / 94.6 (128x256);
+    192 rows 63.2 / 62.4 against 101.2 / 98.5; 256-384 rows 101-119 against
+    140-192)."""
+    if num_experts > 0 and n_size >= 512 and m_total <= 128 * num_experts:
+        return 128, 512
     return 256, 256
 
 
@@ -378,7 +388,7 @@ def persistent_grouped_gemm(
     m_total, k_size = a_cat.shape
     num_experts, _, n_size = b_expert.shape
     if kernel_tile is None:
-        kernel_tile = _default_kernel_tile(m_total, num_experts)
+        kernel_tile = _default_kernel_tile(m_total, num_experts, n_size)
     kbm, kbn = (int(v) for v in kernel_tile)
     if (kbm, kbn) not in _KERNEL_TILES:
         raise ValueError(f"kernel_tile must be one of {_KERNEL_TILES}.")

@@ -109,3 +109,13 @@ def test_large_expert_queue_builds_on_host():
     got = gg._build_work_queue(offs, 300, 128, 256)
     for g, w in zip(got, orc.build_work_queue(offs.numpy(), 300, 128, 256)):
         np.testing.assert_array_equal(g.numpy(), w)
+
+
+def test_default_tile_follows_expert_size():
+    """The drop-in computes with 128x512 when experts hold at most 128 rows on
+    average and N is at least 512, else with 256x256."""
+    assert gg._default_kernel_tile(256 * 128, 256, 2048) == (128, 512)
+    assert gg._default_kernel_tile(64 * 64, 64, 4096) == (128, 512)
+    assert gg._default_kernel_tile(16 * 512, 16, 4096) == (256, 256)
+    assert gg._default_kernel_tile(256 * 128, 256, 256) == (256, 256)
+    assert gg._default_kernel_tile(0, 0, 4096) == (256, 256)

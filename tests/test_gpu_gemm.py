@@ -85,7 +85,7 @@ def test_small_ragged_parity_all_modes(cuda_device, case, dtype):
     counts, k, n = SMALL_CASES[case]
     a, b, offs = make_inputs(counts, k, n, dtype, cuda_device, seed=case, extra_rows=3)
     outs = {}
-    for blocks in [(256, 256), (128, 128), (64, 64), (256, 128), (128, 256), (64, 256)]:
+    for blocks in [(256, 256), (128, 128), (64, 64), (256, 128), (128, 256), (64, 256), (128, 512)]:
         for atomic in (False, True):
             for queue in ("device", "prebuilt"):
                 log(f"case={case} dtype={dtype} blocks={blocks} atomic={atomic} queue={queue}")
@@ -101,7 +101,7 @@ def test_small_ragged_parity_all_modes(cuda_device, case, dtype):
     # partial sums added once: another rounding); it is checked against the
     # oracle above, and repeats itself bitwise.
     mask = torch.from_numpy(covered_rows(offs)).to(cuda_device)
-    for blocks in [(256, 256), (128, 128)]:
+    for blocks in [(256, 256), (128, 128), (128, 512)]:
         ref = outs[(blocks, False, "device")][: mask.numel()][mask]
         for atomic, queue in ((False, "prebuilt"), (True, "prebuilt")):
             got = outs[(blocks, atomic, queue)][: mask.numel()][mask]
@@ -151,7 +151,7 @@ def random_case(seed):
     k = 8 * int(rng.integers(1, 151))
     n = 8 * int(rng.integers(1, 88))
     blocks = [(256, 256), (128, 128), (256, 128), (128, 256), (64, 64), (64, 128), (128, 64),
-              (256, 64), (64, 256)][int(rng.integers(0, 9))]
+              (256, 64), (64, 256), (128, 512)][int(rng.integers(0, 10))]
     return counts.tolist(), k, n, blocks
 
 
@@ -423,7 +423,7 @@ KMAJOR_CASES = [
     ([300, 0, 257, 1, 512], 2056, 264, 0),
 ]
 ALL_BLOCKS = [(256, 256), (128, 128), (256, 128), (128, 256), (64, 64), (64, 128), (128, 64),
-              (256, 64), (64, 256)]
+              (256, 64), (64, 256), (128, 512)]
 
 
 def kmajor_copy(b, pad):
@@ -472,3 +472,31 @@ def test_kmajor_b_fused_epilogues_bitwise(cuda_device, epilogue, block):
     torch.cuda.synchronize()
     mask = torch.from_numpy(covered_rows(offs)).to(cuda_device)
     assert torch.equal(c_k[: mask.numel()][mask], c_n[: mask.numel()][mask])
+
+
+# The 128x512 tile (the default when experts hold at most 128 rows on
+# average): N edges inside and past a 512-wide tile, K tails inside a 32-deep
+# stage, ragged and empty experts, experts above 128 rows (two m-tiles).
+WIDE_CASES = [([128] * 6 + [0, 37], 264, 1000),
+              ([5, 300, 0, 128, 129], 136, 520),
+              ([64] * 12, 2048, 2048),
+              ([1, 2, 3], 40, 512)]
+
+
+@pytest.mark.parametrize("case", range(len(WIDE_CASES)))
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_wide_tile_matches_square_tile(cuda_device, case, dtype):
+    """128x512 against the oracle, and bitwise against the 256x256 tile on
+    striped launches (each output's K sum runs in the same order)."""
+    counts, k, n = WIDE_CASES[case]
+    a, b, offs = make_inputs(counts, k, n, dtype, cuda_device, seed=300 + case, extra_rows=1)
+    mask = torch.from_numpy(covered_rows(offs)).to(cuda_device)
+    square = gg.persistent_grouped_gemm(a, b, offs, kernel_tile=(256, 256), use_atomic_queue=False)
+    for atomic in (False, True):
+        log(f"wide case={case} dtype={dtype} atomic={atomic}")
+        c = gg.persistent_grouped_gemm(a, b, offs, kernel_tile=(128, 512), use_atomic_queue=atomic)
+        torch.cuda.synchronize()
+        assert_parity(c, a, b, offs, k)
+        if not atomic:
+            assert torch.equal(c[: mask.numel()][mask], square[: mask.numel()][mask])
+
