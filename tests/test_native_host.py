@@ -99,7 +99,8 @@ def gemm_call(**over):
 @pytest.mark.parametrize("over, code, text", [
     (dict(dtype=7), nat.MGG_ERR_UNSUPPORTED, b"dtype"),
     (dict(bm=96), nat.MGG_ERR_UNSUPPORTED, b"block_m"),
-    (dict(bn=512), nat.MGG_ERR_UNSUPPORTED, b"block_m"),
+    (dict(bn=1024), nat.MGG_ERR_UNSUPPORTED, b"block_m"),
+    (dict(bm=256, bn=512), nat.MGG_ERR_UNSUPPORTED, b"block_m"),
     # K need not be a multiple of 8 for N-major 16-bit B (A is read to the next
     # multiple, B's rows stop at K), but must be for K-major B.
     (dict(dtype=nat.MGG_DTYPE_BF16 | nat.MGG_B_KMAJOR, k=60, lda=64, ldb_k=64, ldb_e=64 * 64),
