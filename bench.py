@@ -666,7 +666,8 @@ def main():
     offs = gg.expert_offsets_from_recv_counts(case.counts, device=dev)
     atomic = args.mode == "atomic"
     kernel_tile = (_kernel_tile_arg(args.kernel_tile)
-                   or gg._default_kernel_tile(case.m, case.num_experts, case.n))
+                   or gg._default_kernel_tile(case.m, case.num_experts, case.n,
+                                              args.num_sms or gg._cu_count(0)))
     kw = dict(num_sms=args.num_sms, block_m=args.block_m, block_n=args.block_n,
               use_atomic_queue=atomic, kernel_tile=kernel_tile)
 

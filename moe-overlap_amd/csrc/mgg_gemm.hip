@@ -1125,22 +1125,24 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     // col already includes 8*half
     if (row_ok) store_chunk(crow, col, cols, v);
   };
-  // Stores through LDS: a wave's output columns of a row are one 64- or
-  // 128-byte segment of C, but a store instruction straight from the MFMA
+  // Stores through LDS: a wave's output columns of a row are one 64-, 128-
+  // or 256-byte segment of C, but a store instruction straight from the MFMA
   // layout writes 32 rows x 32 bytes.  Each 32-row block instead goes to an
   // LDS region of the wave (row r, 16-byte chunk ch at ch ^ swz(r),
-  // conflict-free both ways) and comes back as whole row segments, 8 rows of
-  // 128 bytes or 16 of 64 per instruction (32 MiB bursts of such stores
-  // measured 30% faster than 32-byte segments; 64-byte ones 19% faster).
-  // The LDS region is free for the whole epilogue:
+  // conflict-free both ways) and comes back as whole row segments, 4 rows of
+  // 256 bytes, 8 of 128 or 16 of 64 per instruction (32 MiB bursts of such
+  // stores measured 30% faster than 32-byte segments for 128 bytes; 64-byte
+  // ones 19% faster).  The LDS region is free for the whole epilogue:
   // * A-block tile: a 4 KiB share of A slot 1.  No DMA is in flight into it
   //   (the last stage's wait retired the zero-fill block the last even stage
   //   sent there) and the next tile first fills it in its first stage, after
   //   the barrier that opens its K loop.
-  // * Other tiles: the wave's own share of buffer 1's A stage.  Every DMA has
-  //   retired before the last stage (its wait is for all of them), and only
-  //   this wave writes that share, with the next tile's stage 1, issued after
-  //   this wave's epilogue.
+  // * Other tiles: the wave's own share of buffer 1's A stage, or for
+  //   256-byte rows (16 rows in each) its shares of buffers 1 and 2's B
+  //   stages.  Every DMA has retired before the last stage (its wait is for
+  //   all of them), and only this wave writes those shares: buffer 1 with the
+  //   next tile's stage 1, issued after this wave's epilogue, buffer 2 with
+  //   stage 2, issued after the next tile's first barrier.
   // The LDS addresses are derived from an opaque copy of the lane index taken
   // in the epilogue: otherwise the compiler computes them once per kernel and
   // keeps them live through the K loop, which then spills.
@@ -1150,17 +1152,23 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // 3.5-5%).
   constexpr int kOutCols = kEpi == kEpiSwiglu ? BN / kWN / 2 : BN / kWN;  // per wave and row
   constexpr int kLineChunks = kOutCols * 2 / 16;  // 16-byte chunks of a wave's row segment
+  // 256-byte rows: the wave's shares of B stages 1 (rows 0-15) and 2 (16-31).
+  constexpr bool kLine256 = kLineChunks == 16 && !kABlk && kStages >= 3 && kBPerWave * 1024 >= 16 * 256;
   constexpr bool kLineStores =
-      (kLineChunks == 4 || kLineChunks == 8) &&
-      (kABlk ? NW * 4096 <= kASlot : kStages >= 2 && kAPerWave * 1024 >= 32 * 16 * kLineChunks);
+      kLine256 || ((kLineChunks == 4 || kLineChunks == 8) &&
+                   (kABlk ? NW * 4096 <= kASlot : kStages >= 2 && kAPerWave * 1024 >= 32 * 16 * kLineChunks));
   const uint32_t line_region =
-      kABlk ? (uint32_t)kASlot + wave * 4096u : (uint32_t)kAStage + wave * (uint32_t)kAPerWave * 1024u;
+      kLine256 ? (uint32_t)(kASlots * kASlot + kBStage) + wave * (uint32_t)kBPerWave * 1024u
+      : kABlk  ? (uint32_t)kASlot + wave * 4096u
+               : (uint32_t)kAStage + wave * (uint32_t)kAPerWave * 1024u;
   auto opaque_lane = [&]() {
     int l = lane;
     asm volatile("" : "+v"(l));
     return l;
   };
   auto line_addr = [&](int r, int ch) {
+    if constexpr (kLine256)
+      return line_region + (uint32_t)((r >> 4) * kBStage + (r & 15) * 256 + ((ch ^ (r & 15)) * 16));
     const int swz = kLineChunks == 8 ? (r >> 1) & 7 : (r >> 2) & 3;
     return line_region + (uint32_t)(r * 16 * kLineChunks + ((ch ^ swz) * 16));
   };

@@ -250,27 +250,34 @@ def _build_work_queue(
 # --------------------------------------------------------------------------
 # grouped GEMM
 # --------------------------------------------------------------------------
-def _default_kernel_tile(m_total: int, num_experts: int, n_size: int = 4096) -> Tuple[int, int]:
-    """128x512 when the experts hold at most 128 rows on average and N is at
-    least 512, else 256x256.  Rows of a tile past its expert's end are
-    zero-fill DMAs that read nothing, so a tile's cost follows the memory
-    requests of its valid rows; both tiles hold the same 256 KiB of fp32
-    accumulators (two waves per SIMD).  With up to 128 rows an expert is one
-    m-tile either way, and the wide tile reads its A rows half as often.
-    Measured on MI355X (HIP-event medians, atomic / striped, µs): E=256 x 128
-    rows, K=7168, N=2048 (the reference benchmark's default problem) 1349 /
-    1332 against 1629 / 1633 (256x256); E=64 x 128, K=N=4096 417 / 404
-    against 472 / 467; E=128 x 64, K=7168, N=2048 626 / 615 against 753 /
-    745; but E=16 x 512, K=2048, N=4096 199 / 188 against 126 / 121 and E=32 x
-    256 205 / 180 against 135 / 133.  Among the tiles of at most 256 rows and
+def _default_kernel_tile(m_total: int, num_experts: int, n_size: int = 4096,
+                         workers: int = 256) -> Tuple[int, int]:
+    """128x512 or 256x256, from the average rows per expert (no host sync on
+    the offsets).  Rows of a tile past its expert's end are zero-fill DMAs that
+    read nothing, so a tile's cost follows the memory requests of its valid
+    rows; both tiles hold the same 256 KiB of fp32 accumulators (two waves per
+    SIMD).  With at most 128 rows an expert is one m-tile either way and the
+    wide tile reads its A rows half as often, but each of its tiles takes about
+    1.6 times as long and there are half as many: it is taken when N >= 512 and
+    1.6 x its rounds of `workers` tiles stay under the square tile's rounds.
+    Measured on MI355X (HIP-event medians, atomic, µs): E=256 x 128 rows,
+    K=7168, N=2048 (the reference benchmark's default problem) 1271 against
+    1584 (256x256); E=128 x 32 rows, K=N=4096, 682 against 776; but E=16 x 128
+    rows, K=2048, N=4096 (128 wide tiles for 256 workers) 74.9 against 57.4;
+    E=64 x 128, N=1024, 80.6 against 60.9; E=16 x 192 and x 256 rows 74.7 and
+    80.1 against 63.0 and 68.8.  Among the tiles of at most 256 rows and
     columns, 256x256 is the fastest at every expert size (E=16, K=2048,
-    N=4096: 64 rows per expert 57.2 / 52.3 against 128x256 63.4 / 54.5 and
-    128x128 55.4 / 50.9; 128 rows 60.9 / 60.5 against 95.5 / 94.6 (128x256);
-    192 rows 63.2 / 62.4 against 101.2 / 98.5; 256-384 rows 101-119 against
-    140-192)."""
-    if num_experts > 0 and n_size >= 512 and m_total <= 128 * num_experts:
-        return 128, 512
-    return 256, 256
+    N=4096, atomic / striped: 64 rows per expert 57.2 / 52.3 against 128x256
+    63.4 / 54.5 and 128x128 55.4 / 50.9; 128 rows 60.9 / 60.5 against 95.5 /
+    94.6 (128x256); 192 rows 63.2 / 62.4 against 101.2 / 98.5; 256-384 rows
+    101-119 against 140-192)."""
+    if num_experts <= 0 or n_size < 512 or m_total > 128 * num_experts:
+        return 256, 256
+    rows = max(-(-m_total // num_experts), 1)
+    w = max(int(workers), 1)
+    rounds_wide = -(-(num_experts * -(-rows // 128) * -(-n_size // 512)) // w)
+    rounds_square = -(-(num_experts * -(-rows // 256) * -(-n_size // 256)) // w)
+    return (128, 512) if 1.6 * rounds_wide < rounds_square else (256, 256)
 
 
 def _requested_tile(block_m, block_n) -> Tuple[int, int]:
@@ -387,17 +394,17 @@ def persistent_grouped_gemm(
 
     m_total, k_size = a_cat.shape
     num_experts, _, n_size = b_expert.shape
-    if kernel_tile is None:
-        kernel_tile = _default_kernel_tile(m_total, num_experts, n_size)
-    kbm, kbn = (int(v) for v in kernel_tile)
-    if (kbm, kbn) not in _KERNEL_TILES:
-        raise ValueError(f"kernel_tile must be one of {_KERNEL_TILES}.")
     device = a_cat.device
     dev_index = device.index if device.index is not None else torch.cuda.current_device()
     if num_sms is None:
         num_sms = _cu_count(dev_index)
     if int(num_sms) <= 0:
         raise ValueError("num_sms must be positive.")
+    if kernel_tile is None:
+        kernel_tile = _default_kernel_tile(m_total, num_experts, n_size, int(num_sms))
+    kbm, kbn = (int(v) for v in kernel_tile)
+    if (kbm, kbn) not in _KERNEL_TILES:
+        raise ValueError(f"kernel_tile must be one of {_KERNEL_TILES}.")
     counter_dev = _counter_arg(work_counter, use_atomic_queue, device)
 
     # K not a multiple of 8: A is zero-padded on the device to the next

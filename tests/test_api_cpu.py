@@ -113,9 +113,14 @@ def test_large_expert_queue_builds_on_host():
 
 def test_default_tile_follows_expert_size():
     """The drop-in computes with 128x512 when experts hold at most 128 rows on
-    average and N is at least 512, else with 256x256."""
-    assert gg._default_kernel_tile(256 * 128, 256, 2048) == (128, 512)
-    assert gg._default_kernel_tile(64 * 64, 64, 4096) == (128, 512)
-    assert gg._default_kernel_tile(16 * 512, 16, 4096) == (256, 256)
-    assert gg._default_kernel_tile(256 * 128, 256, 256) == (256, 256)
+    average, N is at least 512, and the wide tiles fill enough rounds of the
+    workers (1.6 x its rounds under the square tile's), else with 256x256."""
+    assert gg._default_kernel_tile(256 * 128, 256, 2048) == (128, 512)   # 4 rounds against 8
+    assert gg._default_kernel_tile(128 * 32, 128, 4096) == (128, 512)    # 4 against 8
+    assert gg._default_kernel_tile(16 * 128, 16, 4096) == (256, 256)     # 1 against 1
+    assert gg._default_kernel_tile(64 * 128, 64, 1024) == (256, 256)     # 1 against 1
+    assert gg._default_kernel_tile(16 * 512, 16, 4096) == (256, 256)     # 512 rows
+    assert gg._default_kernel_tile(256 * 128, 256, 256) == (256, 256)    # N < 512
     assert gg._default_kernel_tile(0, 0, 4096) == (256, 256)
+    assert gg._default_kernel_tile(256 * 128, 256, 2048, workers=1024) == (128, 512)  # 1 against 2
+    assert gg._default_kernel_tile(256 * 128, 256, 2048, workers=2048) == (256, 256)  # 1 against 1
