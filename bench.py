@@ -498,6 +498,16 @@ def reference_bench_summary(dev, dtype, num_sms=None, steps=30):
                              "frac_of_hbm_roofline": round(t_hbm / t, 4),
                              "flushed_kernel_ms_median": round(tc, 4),
                              "flushed_frac_of_hbm_roofline": round(t_hbm / tc, 4)}
+    # The vendor library's batched GEMM (torch.bmm -> hipBLASLt) on the same
+    # operands (equal counts make the problem one batched GEMM), for reference.
+    a3 = case.a.view(case.num_experts, int(case.counts[0]), case.k)
+    bmm = lambda: torch.bmm(a3, case.b)
+    settle_clock(bmm)
+    tb = median(event_times_ms(bmm, steps))
+    out["hipblaslt_bmm"] = {"kernel_ms_median": round(tb, 4),
+                            "frac_of_hbm_roofline": round(t_hbm / tb, 4)}
+    out["kernel_tile"] = "{}x{}".format(*gg._default_kernel_tile(
+        case.m, case.num_experts, case.n, num_sms or gg._cu_count(dev.index or 0)))
     c = gg.persistent_grouped_gemm(case.a, case.b, offs, num_sms=num_sms)
     rows = torch.arange(0, case.m, 509, device=dev)
     e_of = torch.div(rows, int(case.counts[0]), rounding_mode="floor")
@@ -773,22 +783,26 @@ def main():
             extra["hipblaslt_bmm_ms_median"] = round(median(tb), 4)
             extra["hipblaslt_bmm_tflops"] = round(flops / (median(tb) * 1e-3) / 1e12, 1)
         # N not a multiple of 8 is read and written in place: N = 4092 against
-        # N = 4096 on the metric's other dimensions.
+        # N = 4096 on the metric's other dimensions, timed in alternating
+        # batches so a drifting clock weighs on both alike.
         progress("odd-N leg")
-        odd = {}
+        legs_n = {}
         for n_odd in (4096, 4092):
             co = workloads.uniform_case(case.num_experts, int(case.counts[0]), case.k, n_odd)
             workloads.fill_operands(co, device=dev, dtype=dtype)
             oo = gg.expert_offsets_from_recv_counts(co.counts, device=dev)
-            fn = lambda: gg.persistent_grouped_gemm(co.a, co.b, oo, num_sms=args.num_sms,
-                                                    use_atomic_queue=atomic)
-            settle_clock(fn)
-            t = median(event_times_ms(fn, 50))
-            odd[f"n{n_odd}"] = {"kernel_ms_median": round(t, 5),
-                                "tflops": round(co.flops / (t * 1e-3) / 1e12, 1)}
-            del co, oo
-        odd["ratio_4092_over_4096"] = round(odd["n4092"]["kernel_ms_median"]
-                                            / odd["n4096"]["kernel_ms_median"], 4)
+            legs_n[n_odd] = (co, (lambda co=co, oo=oo: gg.persistent_grouped_gemm(
+                co.a, co.b, oo, num_sms=args.num_sms, use_atomic_queue=atomic)))
+        settle_clock(legs_n[4096][1])
+        times_n = {4096: [], 4092: []}
+        for rnd in range(10):
+            for n_odd in ((4096, 4092) if rnd % 2 == 0 else (4092, 4096)):
+                times_n[n_odd] += batched_times_ms(legs_n[n_odd][1], launches=20, batch=10)
+        odd = {f"n{n_odd}": {"kernel_ms_median": round(median(t), 5),
+                             "tflops": round(legs_n[n_odd][0].flops / (median(t) * 1e-3) / 1e12, 1)}
+               for n_odd, t in times_n.items()}
+        odd["ratio_4092_over_4096"] = round(median(times_n[4092]) / median(times_n[4096]), 4)
+        del legs_n
         extra["n_not_multiple_of_8"] = odd
         progress("overlap leg")
         extra["overlap"] = overlap_summary(case, offs, dev)
