@@ -172,7 +172,7 @@ int mgg_build_work_queue_host(const int64_t* expert_offsets, int64_t num_experts
  * If the queue is empty, C is zero-filled; with K == 0 the covered rows are
  * zeros (A and B and their strides are not read).  Rows of C not covered by
  * any expert range are left unwritten.  Supported: dtype BF16/FP16,
- * block_m, block_n in {64, 128, 256}, N even (B's and C's rows are read and
+ * block_m, block_n in {64, 128, 256} or 128 x 512, N even (B's and C's rows are read and
  * written at any 4-byte alignment; the last chunk of a C row is stored by
  * words), lda (and ldb_k of K-major B) a multiple of 8 elements, ldb_k of
  * N-major B, ldb_e and ldc even, 16-byte aligned base pointers, E <= 2048
@@ -312,9 +312,10 @@ int mgg_debug_set_split_flags(uint64_t value, void* stream);
  * whole, bitwise the striped schedule's results); 1 turns it back on (the
  * default).  mgg_reserve_split_workspace makes the workspace of `stream` on
  * the current device now, so no launch allocates it (otherwise the first
- * atomic launch on the stream that could split does); it is never freed.
- * At most 16 streams per device get one; launches on further streams, and
- * launches under graph capture, take every tile whole.
+ * atomic launch on the stream that could split does); it is never freed,
+ * and it cannot be made under graph capture (MGG_ERR_INVALID).  At most 16
+ * streams per device get one; launches on further streams, and launches
+ * under graph capture, take every tile whole.
  * mgg_split_workspace_bytes reports the bytes held for `stream` (0: none).
  */
 int mgg_set_split_last_round(int enabled);

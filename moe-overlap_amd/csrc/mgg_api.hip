@@ -479,7 +479,7 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
                          (block_n == 64 || block_n == 128 || block_n == 256)) ||
                         (block_m == 128 && block_n == 512);
   if (!fp8 && !block_ok)  // fp8 tiles were checked above
-    return set_error(MGG_ERR_UNSUPPORTED, "block_m/block_n must each be one of 64, 128, 256");
+    return set_error(MGG_ERR_UNSUPPORTED, "block_m/block_n must each be one of 64, 128, 256, or be 128 x 512");
   if (!epilogue_supported(epilogue, block_m, block_n))
     return set_error(MGG_ERR_UNSUPPORTED, "fused epilogues need block_m == block_n in {128, 256}");
   if (m_size < 0 || k_size < 0 || n_size < 0 || num_experts < 0)
@@ -712,8 +712,16 @@ int mgg_debug_counter_slots(int device, int* held) {
 
 int mgg_reserve_split_workspace(void* stream) {
   mgg::clear_error();
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (st != nullptr) {  // (allocating, and clearing the flags, under capture would be recorded)
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    const hipError_t err = hipStreamIsCapturing(st, &capture);
+    if (err != hipSuccess) return mgg::hip_error(err, "hipStreamIsCapturing");
+    if (capture != hipStreamCaptureStatusNone)
+      return set_error(MGG_ERR_INVALID, "the split workspace cannot be reserved under graph capture");
+  }
   const mgg::SplitSpace* sp = nullptr;
-  return mgg::split_space(static_cast<hipStream_t>(stream), true, &sp);
+  return mgg::split_space(st, true, &sp);
 }
 
 int mgg_split_workspace_bytes(void* stream, int64_t* bytes) {

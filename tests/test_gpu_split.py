@@ -212,6 +212,22 @@ def test_captured_split_call_agrees_with_eager(cuda_device):
     assert_parity(captured, a, b, offs, k)
 
 
+def test_reserve_split_workspace_refused_under_capture(cuda_device):
+    """Reserving the workspace would allocate and clear flags inside the
+    capture: refused with an error, the capture itself unharmed."""
+    counts, k, n, g = CASES[0]
+    a, b, offs = make_inputs(counts, k, n, torch.bfloat16, cuda_device, seed=3)
+    striped = gg.persistent_grouped_gemm(a, b, offs, num_sms=g, use_atomic_queue=False)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        with pytest.raises(nat.NativeError, match="graph capture"):
+            gg.reserve_split_workspace(cuda_device)
+        captured = gg.persistent_grouped_gemm(a, b, offs, num_sms=g)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(captured, striped)
+
+
 def test_split_workspace_is_one_slot_per_cu(cuda_device):
     """The split workspace of a stream holds one 256 x 256 fp32 slot and one
     flag word per CU, whatever the worker count: 64 MiB on a 256-CU device
