@@ -782,26 +782,29 @@ def main():
             tb = event_times_ms(bmm, 50)
             extra["hipblaslt_bmm_ms_median"] = round(median(tb), 4)
             extra["hipblaslt_bmm_tflops"] = round(flops / (median(tb) * 1e-3) / 1e12, 1)
-        # N not a multiple of 8 is read and written in place: N = 4092 against
-        # N = 4096 on the metric's other dimensions, timed in alternating
-        # batches so a drifting clock weighs on both alike.
+        # N not a multiple of 8 is read and written in place: N = 4092 and the
+        # odd N = 4095 (its own kernel instance) against N = 4096 on the
+        # metric's other dimensions, timed in rotating batches so a drifting
+        # clock weighs on all alike.
         progress("odd-N leg")
+        ns = (4096, 4092, 4095)
         legs_n = {}
-        for n_odd in (4096, 4092):
+        for n_odd in ns:
             co = workloads.uniform_case(case.num_experts, int(case.counts[0]), case.k, n_odd)
             workloads.fill_operands(co, device=dev, dtype=dtype)
             oo = gg.expert_offsets_from_recv_counts(co.counts, device=dev)
             legs_n[n_odd] = (co, (lambda co=co, oo=oo: gg.persistent_grouped_gemm(
                 co.a, co.b, oo, num_sms=args.num_sms, use_atomic_queue=atomic)))
         settle_clock(legs_n[4096][1])
-        times_n = {4096: [], 4092: []}
-        for rnd in range(10):
-            for n_odd in ((4096, 4092) if rnd % 2 == 0 else (4092, 4096)):
+        times_n = {n_odd: [] for n_odd in ns}
+        for rnd in range(12):
+            for n_odd in ns[rnd % 3:] + ns[:rnd % 3]:
                 times_n[n_odd] += batched_times_ms(legs_n[n_odd][1], launches=20, batch=10)
         odd = {f"n{n_odd}": {"kernel_ms_median": round(median(t), 5),
                              "tflops": round(legs_n[n_odd][0].flops / (median(t) * 1e-3) / 1e12, 1)}
                for n_odd, t in times_n.items()}
         odd["ratio_4092_over_4096"] = round(median(times_n[4092]) / median(times_n[4096]), 4)
+        odd["ratio_4095_over_4096"] = round(median(times_n[4095]) / median(times_n[4096]), 4)
         del legs_n
         extra["n_not_multiple_of_8"] = odd
         progress("overlap leg")

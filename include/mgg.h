@@ -172,19 +172,21 @@ int mgg_build_work_queue_host(const int64_t* expert_offsets, int64_t num_experts
  * If the queue is empty, C is zero-filled; with K == 0 the covered rows are
  * zeros (A and B and their strides are not read).  Rows of C not covered by
  * any expert range are left unwritten.  Supported: dtype BF16/FP16,
- * block_m, block_n in {64, 128, 256} or 128 x 512, N even (B's and C's rows are read and
- * written at any 4-byte alignment; the last chunk of a C row is stored by
- * words), lda (and ldb_k of K-major B) a multiple of 8 elements, ldb_k of
- * N-major B, ldb_e and ldc even, 16-byte aligned base pointers, E <= 2048
- * when the queue is derived on the device.  K % 8 == 0 for K-major B; with
- * N-major B any K:
+ * block_m, block_n in {64, 128, 256} or 128 x 512, any N (B's and C's rows
+ * are read and written at any 2-byte alignment; the last chunk of a C row
+ * is stored by pairs and, for odd N, one 2-byte store), lda (and ldb_k of
+ * K-major B) a multiple of 8 elements, any ldb_k of N-major B, ldb_e and
+ * ldc, 16-byte aligned base pointers, E <= 2048 when the queue is derived
+ * on the device.  B must span its view: (E-1)*ldb_e + (K-1)*ldb_k + N
+ * elements for N-major B (ldb_e may be 0: every expert shares one B).
+ * K % 8 == 0 for K-major B; with N-major B any K:
  * B's rows at and past K are never read (they count as zeros), while A is
  * read up to the next multiple of 8, so lda must cover it and A's elements
  * in those columns must be finite (they are multiplied by zeros; the drop-in
  * makes them zeros).
  * (ABI version 4 added report_block_m, report_block_n; version 6 any K for
  * N-major B; version 7 the split controls, per-capture counter words and
- * any even N.)
+ * any even N; version 8 odd N and any B and C strides.)
  */
 int mgg_grouped_gemm(int dtype, const void* a, const void* b, void* c,
                      const int32_t* expert_offsets, int64_t m_size, int64_t k_size, int64_t n_size,
@@ -247,10 +249,10 @@ int mgg_grouped_gemm_gathered(int dtype, int epilogue, const void* a, const int3
  *   c  [M, N]     BF16, row stride ldc
  * Queue (derived on the device, or prebuilt), schedules, work_counter and
  * empty-queue behaviour as in mgg_grouped_gemm.  Tiles 256x256, 256x128,
- * 192x128 and 128x128; K, lda, ldb_n, ldb_e multiples of 16; N, ldc
- * even.
+ * 192x128 and 128x128; K, lda, ldb_n, ldb_e multiples of 16; any N and
+ * ldc.
  * (Introduced with ABI version 2; version 4 added the queue and report-tile
- * arguments.)
+ * arguments; version 8 odd N and any ldc.)
  */
 int mgg_grouped_gemm_fp8(const void* a, const void* b, void* c, const int32_t* expert_offsets,
                          const float* a_scale, const float* b_scale, int64_t m_size,

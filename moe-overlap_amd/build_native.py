@@ -17,7 +17,7 @@ REPO_DIR = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 BUILD_DIR = REPO_DIR / "_build"
 LIB_PATH = PKG_DIR / "libmgg.so"
-SOURCES = ("mgg_api.hip", "mgg_gemm.hip", "mgg_queue.hip", "mgg_moe.hip")
+SOURCES = ("mgg_api.hip", "mgg_gemm.hip", "mgg_gemm_odd.hip", "mgg_queue.hip", "mgg_moe.hip")
 
 ARCH = "gfx950"
 HIP_FLAGS = [

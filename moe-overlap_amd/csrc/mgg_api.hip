@@ -346,7 +346,7 @@ using mgg::set_error;
 
 extern "C" {
 
-int mgg_abi_version(void) { return 7; }
+int mgg_abi_version(void) { return 8; }
 
 const char* mgg_last_error(void) { return mgg::g_last_error.c_str(); }
 
@@ -485,17 +485,23 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   if (m_size < 0 || k_size < 0 || n_size < 0 || num_experts < 0)
     return set_error(MGG_ERR_INVALID, "sizes must be >= 0");
   if (m_size == 0 || n_size == 0) return MGG_OK;  // C has no elements
-  // N even: B's and C's rows need not be 16-byte aligned (16-byte DMAs and
+  // Any N: B's and C's rows need not be 16-byte aligned (16-byte DMAs and
   // stores run at any 2-byte alignment); the last chunk of a row is read as
-  // it lies and stored by words.  (With N odd the word holding B's last
-  // element would straddle the end of its buffer descriptor, where the range
-  // check zeroes the whole word.)
-  if (n_size % 2 != 0) return set_error(MGG_ERR_UNSUPPORTED, "N must be even");
+  // it lies and stored by pairs and, for odd N, one 2-byte store.  (With N
+  // odd the dword holding B's last element straddles the end of B's view;
+  // the kernel adds that element's term separately.)  Odd N runs on kernel
+  // instances of its own, compiled for fewer tiles.
+  const bool odd_n = (n_size & 1) != 0;
+  if (odd_n && !((block_m == 256 && block_n == 256) || (block_m == 128 && block_n == 128) ||
+                 (block_m == 128 && block_n == 512 && !b_rows_k && epilogue == MGG_EPI_NONE)))
+    return set_error(MGG_ERR_UNSUPPORTED,
+                     "odd N runs on 256x256 and 128x128 tiles (and 128x512 for N-major 16-bit B "
+                     "without a fused epilogue)");
   // K not a multiple of 8 (16-bit N-major B only): A is read to the next
   // multiple of 8 (those columns meet B rows that read as zeros), B's rows
   // stop at K.
   if (k_size % 8 != 0 && (fp8 || b_rows_k))
-    return set_error(MGG_ERR_UNSUPPORTED, "K and N must be multiples of 8 (K-major B, fp8)");
+    return set_error(MGG_ERR_UNSUPPORTED, "K must be a multiple of 8 (K-major B, fp8)");
   const int64_t k_a = (k_size + 7) / 8 * 8;
   // K == 0: nothing is read (every DMA is past its descriptor, so the tiles
   // hold zeros); A's and B's strides are then unused.
@@ -515,10 +521,9 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
   if (report_block_n <= 0) report_block_n = block_n;
   if (lda < k_a || ldb_k < (b_rows_k ? k_size : n_size) || ldc < c_cols || ldb_e < 0)
     return set_error(MGG_ERR_INVALID, "leading dimensions smaller than the matrix extents");
-  if (lda % 8 != 0 || ldb_k % (b_rows_k ? 8 : 2) != 0 || ldb_e % 2 != 0 || ldc % 2 != 0)
+  if (lda % 8 != 0 || (b_rows_k && ldb_k % 8 != 0))
     return set_error(MGG_ERR_UNSUPPORTED,
-                     "strides must be multiples of 8 elements (lda; ldb_k of K-major B) or of 2 "
-                     "(ldb_k of N-major B, ldb_e, ldc)");
+                     "lda (and ldb_k of K-major B) must be a multiple of 8 elements");
   // A and B may be null only when nothing reads them (no experts or K == 0).
   const bool reads_ab = num_experts > 0 && k_size > 0;
   if (c == nullptr || expert_offsets == nullptr || (reads_ab && (a == nullptr || b == nullptr)))
@@ -606,7 +611,8 @@ int grouped_gemm_impl(int dtype, int epilogue, const void* a, const void* b, voi
       if (rc != MGG_OK) return rc;
     }
   }
-  return launch_grouped_gemm(dtype, epilogue, block_m, block_n, p, workers, st);
+  return odd_n ? launch_grouped_gemm_odd(dtype, epilogue, block_m, block_n, p, workers, st)
+               : launch_grouped_gemm(dtype, epilogue, block_m, block_n, p, workers, st);
 }
 
 }  // namespace

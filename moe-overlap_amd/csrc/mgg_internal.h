@@ -29,6 +29,10 @@ constexpr int kEpiSwiglu = 2;
 // OR'd into a kernel's epilogue template argument (never an MGG_EPI_* value):
 // the instance that reads A's rows through GemmParams::a_rows.
 constexpr int kEpiGather = 4;
+// Likewise: the instance for odd N (C's rows end in a 2-byte store; with
+// N-major 16-bit B the term of B's last element is added separately).  Even
+// N runs instances without it, whose code carries none of this.
+constexpr int kEpiOddN = 8;
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -94,6 +98,11 @@ unsigned long long* clock_probe();
 // `stream` with `workers` workgroups.  Returns MGG_OK or an error code.
 int launch_grouped_gemm(int dtype, int epilogue, int block_m, int block_n, const GemmParams& p,
                         int workers, hipStream_t stream);
+// The same for odd N (p.n odd), on the tiles compiled for it: 256x256 and
+// 128x128, and 128x512 for 16-bit types without a fused epilogue; other
+// requested tiles compute on the nearest of these.
+int launch_grouped_gemm_odd(int dtype, int epilogue, int block_m, int block_n, const GemmParams& p,
+                            int workers, hipStream_t stream);
 // Whether a fused epilogue is compiled for this tile shape.
 bool epilogue_supported(int epilogue, int block_m, int block_n);
 

@@ -201,12 +201,11 @@ def expert_mlp_forward(
 
 def _gathered_ok(x, w1, block):
     """Whether the up GEMM can read its A rows from x in place: the 256x256
-    tile with N-major weights, the device-derived queue, 16-byte aligned rows
-    and 32-bit offsets into x."""
+    tile with N-major weights (any N and strides), the device-derived queue,
+    16-byte aligned rows of x and 32-bit offsets into x."""
     return (block == 256 and w1.shape[0] <= nat.MAX_DEVICE_QUEUE_EXPERTS
             and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
-            and w1.stride(2) == 1 and w1.stride(1) % 8 == 0 and w1.stride(0) % 8 == 0
-            and w1.data_ptr() % 16 == 0 and x.shape[1] % 8 == 0 and w1.shape[2] % 8 == 0
+            and w1.stride(2) == 1 and w1.data_ptr() % 16 == 0 and x.shape[1] % 8 == 0
             and (x.shape[0] * x.stride(0) + x.shape[1]) * 2 < (1 << 31) - 4096)
 
 

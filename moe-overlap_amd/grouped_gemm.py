@@ -47,9 +47,9 @@ Differences, all in arguments that do not change results:
 * Operands whose inner stride is not 1 are copied on the device first, and
   so is A when its row stride is not a multiple of 8 elements.  K not a multiple of 8: A is copied with
   zero columns to the next multiple of 8 and B is read in place (the kernel
-  stops B's rows at K; a K-major B view is copied).  Any even N is read and
-  written in place (B's and C's rows need not be 16-byte aligned); odd N: B
-  is copied with one zero column and C sliced.  K == 0 gives zeros, as there.
+  stops B's rows at K; a K-major B view is copied).  Any N is read and
+  written in place (B's and C's rows need not be 16-byte aligned).  K == 0
+  gives zeros, as there.
 """
 from __future__ import annotations
 
@@ -298,8 +298,8 @@ def _requested_tile(block_m, block_n) -> Tuple[int, int]:
 
 def _fast_layout(t: torch.Tensor, mult: int = 8) -> bool:
     """Unit inner stride, 16-byte aligned base, outer strides multiples of
-    `mult` elements (8 for A; 2 for N-major B, whose rows the kernel reads at
-    any 4-byte alignment)."""
+    `mult` elements (8 for A; 1 for N-major B, whose rows the kernel reads at
+    any 2-byte alignment)."""
     if t.stride(-1) != 1 or t.data_ptr() % 16 != 0:
         return False
     return all(t.stride(d) % mult == 0 for d in range(t.dim() - 1) if t.size(d) > 1)
@@ -315,6 +315,16 @@ def _kmajor_layout(b: torch.Tensor) -> bool:
     if b.data_ptr() % 16 != 0 or b.stride(2) % 8 != 0:
         return False
     return b.size(0) < 2 or b.stride(0) % 8 == 0
+
+
+def _odd_n_tile(tile: Tuple[int, int], wide_ok: bool) -> Tuple[int, int]:
+    """Odd N runs on kernel instances of its own, compiled for 256x256 and
+    128x128 tiles (and 128x512 when `wide_ok`: N-major 16-bit B): another
+    kernel tile computes on the nearest of these (the requested tile still
+    sets the queue the work_counter counts)."""
+    if tile in ((256, 256), (128, 128)) or (wide_ok and tile == (128, 512)):
+        return tile
+    return (256, 256) if max(tile) >= 256 else (128, 128)
 
 
 def _gemm_operand(t: torch.Tensor, mult: int = 8) -> torch.Tensor:
@@ -409,49 +419,44 @@ def persistent_grouped_gemm(
 
     # K not a multiple of 8: A is zero-padded on the device to the next
     # multiple of 8 and B is read as it lies (the kernel stops B's rows at K,
-    # so the padding columns meet zeros).  Even N: B and C are used as they
-    # lie (the kernel reads and writes rows at any 4-byte alignment).  Odd N:
-    # B is zero-padded by one column and C sliced (the word holding B's last
-    # element would straddle the end of the kernel's buffer descriptor).
+    # so the padding columns meet zeros).  Any N: B and C are used as they
+    # lie (the kernel reads and writes rows at any 2-byte alignment).
     k_pad = (k_size + 7) // 8 * 8
-    n_pad = n_size + (n_size & 1)
     a_op, b_op = a_cat, b_expert
     # B stored [E, N, K] is read as it lies (no transposing copy).
-    b_kmajor = k_pad == k_size and n_pad == n_size and _kmajor_layout(b_expert)
+    b_kmajor = k_pad == k_size and _kmajor_layout(b_expert)
+    if n_size & 1:
+        kbm, kbn = _odd_n_tile((kbm, kbn), not b_kmajor)
     if k_pad != k_size:
         a_op = torch.nn.functional.pad(a_op, (0, k_pad - k_size))
-    if n_pad != n_size:
-        b_op = torch.nn.functional.pad(b_op, (0, n_pad - n_size))
     if k_pad > 0:
         a_op = _gemm_operand(a_op)
         if not b_kmajor:
-            b_op = _gemm_operand(b_op, 2)
+            b_op = _gemm_operand(b_op, 1)
     # Leading dimensions; a size-1 dimension's stride is never used, nor are
     # A's and B's when K == 0.  ldb_k is the stride between B's rows: K rows,
     # or N rows for K-major B.
     lda = a_op.stride(0) if m_total > 1 else k_pad
     if b_kmajor:
         ldb_k = b_op.stride(2)
-        ldb_e = b_op.stride(0) if num_experts > 1 else n_pad * ldb_k
+        ldb_e = b_op.stride(0) if num_experts > 1 else n_size * ldb_k
     else:
-        ldb_k = b_op.stride(1) if k_size > 1 else n_pad
+        ldb_k = b_op.stride(1) if k_size > 1 else n_size
         ldb_e = b_op.stride(0) if num_experts > 1 else k_size * ldb_k
     dtype_code = _DTYPE_CODES[a_cat.dtype] | (_nat.MGG_B_KMAJOR if b_kmajor else 0)
-    c_op = torch.empty((m_total, n_pad), device=device, dtype=a_cat.dtype)
+    c_op = torch.empty((m_total, n_size), device=device, dtype=a_cat.dtype)
 
     we, wm, wn, num_work = _queue_args(queue, expert_offsets, n_size, kbm, kbn)
     off32 = _offsets_i32(expert_offsets)
     args = (
         dtype_code, _ptr(a_op), _ptr(b_op), _ptr(c_op),
-        _ptr(off32), m_total, k_size, n_pad,
+        _ptr(off32), m_total, k_size, n_size,
         num_experts, lda, ldb_e, ldb_k, c_op.stride(0),
         _ptr(we), _ptr(wm), _ptr(wn), num_work,
         kbm, kbn, int(num_sms), 1 if use_atomic_queue else 0,
         _ptr(counter_dev), rep_m, rep_n, torch.cuda.current_stream(device).cuda_stream,
     )
     _launch(_nat.lib().mgg_grouped_gemm, args, dev_index)
-    if n_pad != n_size:
-        return c_op[:, :n_size].contiguous()
     return c_op
 
 
@@ -535,6 +540,8 @@ def _persistent_grouped_gemm_fp8(a_cat, b_expert, expert_offsets, a_scale, b_sca
     kbm, kbn = (int(v) for v in kernel_tile)
     if (kbm, kbn) not in _FP8_KERNEL_TILES:
         raise ValueError(f"fp8 kernel_tile must be one of {_FP8_KERNEL_TILES}.")
+    if n_size & 1:
+        kbm, kbn = _odd_n_tile((kbm, kbn), False)
     if queue == "device" and num_experts > _nat.MAX_DEVICE_QUEUE_EXPERTS:
         queue = "prebuilt"
     if num_sms is None:
@@ -542,40 +549,34 @@ def _persistent_grouped_gemm_fp8(a_cat, b_expert, expert_offsets, a_scale, b_sca
     if int(num_sms) <= 0:
         raise ValueError("num_sms must be positive.")
     counter_dev = _counter_arg(work_counter, use_atomic_queue, device)
-    # K to a multiple of 16, N to an even count (zero padding adds nothing).
+    # K to a multiple of 16 (zero padding adds nothing); any N.
     k_pad = (k_size + 15) // 16 * 16
-    n_pad = n_size + (n_size & 1)
     a_op = a_cat
     if k_pad != k_size:
         a_op = torch.nn.functional.pad(a_op.view(torch.uint8), (0, k_pad - k_size)).view(a_cat.dtype)
     if k_pad > 0 and (a_op.stride(1) != 1 or a_op.stride(0) % 16 or a_op.data_ptr() % 16):
         a_op = a_op.contiguous()
     b_nk = b_expert.transpose(1, 2)  # [E, N, K]
-    if k_pad != k_size or n_pad != n_size:
+    if k_pad != k_size:
         b_nk = torch.nn.functional.pad(b_nk.contiguous().view(torch.uint8),
-                                       (0, k_pad - k_size, 0, n_pad - n_size)).view(b_expert.dtype)
+                                       (0, k_pad - k_size)).view(b_expert.dtype)
     if k_pad > 0 and (b_nk.stride(2) != 1 or b_nk.stride(1) % 16 or b_nk.stride(0) % 16
                       or b_nk.data_ptr() % 16):
         b_nk = b_nk.contiguous()
     sa = a_scale.reshape(-1).to(torch.float32).contiguous()
-    sb = b_scale.reshape(num_experts, n_size).to(torch.float32)
-    if n_pad != n_size:
-        sb = torch.nn.functional.pad(sb, (0, n_pad - n_size))
-    sb = sb.contiguous()
+    sb = b_scale.reshape(num_experts, n_size).to(torch.float32).contiguous()
     off32 = _offsets_i32(expert_offsets)
-    c_op = torch.empty((m_total, n_pad), device=device, dtype=torch.bfloat16)
+    c_op = torch.empty((m_total, n_size), device=device, dtype=torch.bfloat16)
     lda = a_op.stride(0) if m_total > 1 else k_pad
-    ldb_n = b_nk.stride(1) if n_pad > 1 else k_pad
-    ldb_e = b_nk.stride(0) if num_experts > 1 else n_pad * ldb_n
+    ldb_n = b_nk.stride(1) if n_size > 1 else k_pad
+    ldb_e = b_nk.stride(0) if num_experts > 1 else n_size * ldb_n
     we, wm, wn, num_work = _queue_args(queue, expert_offsets, n_size, kbm, kbn)
     args = (_ptr(a_op), _ptr(b_nk), _ptr(c_op), _ptr(off32), _ptr(sa), _ptr(sb),
-            m_total, k_pad, n_pad, num_experts, lda, ldb_e, ldb_n, c_op.stride(0),
+            m_total, k_pad, n_size, num_experts, lda, ldb_e, ldb_n, c_op.stride(0),
             _ptr(we), _ptr(wm), _ptr(wn), num_work,
             kbm, kbn, int(num_sms), 1 if use_atomic_queue else 0,
             _ptr(counter_dev), rep_m, rep_n, torch.cuda.current_stream(device).cuda_stream)
     _launch(_nat.lib().mgg_grouped_gemm_fp8, args, dev_index)
-    if n_pad != n_size:
-        return c_op[:, :n_size].contiguous()
     return c_op
 
 

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime this library must share)
 
 LIB_PATH = Path(__file__).resolve().parent / "libmgg.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 MGG_OK = 0
 MGG_ERR_INVALID = 1

@@ -124,3 +124,16 @@ def test_default_tile_follows_expert_size():
     assert gg._default_kernel_tile(0, 0, 4096) == (256, 256)
     assert gg._default_kernel_tile(256 * 128, 256, 2048, workers=1024) == (128, 512)  # 1 against 2
     assert gg._default_kernel_tile(256 * 128, 256, 2048, workers=2048) == (256, 256)  # 1 against 1
+
+
+def test_odd_n_tiles():
+    """Odd N computes on the tiles its kernel instances are compiled for."""
+    for t in ((256, 256), (128, 128)):
+        assert gg._odd_n_tile(t, True) == t and gg._odd_n_tile(t, False) == t
+    assert gg._odd_n_tile((128, 512), True) == (128, 512)
+    assert gg._odd_n_tile((128, 512), False) == (256, 256)
+    assert gg._odd_n_tile((256, 128), True) == (256, 256)
+    assert gg._odd_n_tile((64, 256), True) == (256, 256)
+    assert gg._odd_n_tile((192, 128), False) == (128, 128)
+    for t in ((64, 64), (128, 64), (64, 128)):
+        assert gg._odd_n_tile(t, True) == (128, 128)

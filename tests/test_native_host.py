@@ -104,14 +104,22 @@ def gemm_call(**over):
     # K need not be a multiple of 8 for N-major 16-bit B (A is read to the next
     # multiple, B's rows stop at K), but must be for K-major B.
     (dict(dtype=nat.MGG_DTYPE_BF16 | nat.MGG_B_KMAJOR, k=60, lda=64, ldb_k=64, ldb_e=64 * 64),
-     nat.MGG_ERR_UNSUPPORTED, b"multiples of 8"),
+     nat.MGG_ERR_UNSUPPORTED, b"multiple of 8"),
     (dict(k=60, lda=56), nat.MGG_ERR_INVALID, b"leading"),
-    # N even is read in place (n=60 passes this check); odd N is not.
-    (dict(n=61, ldb_k=64, ldc=64), nat.MGG_ERR_UNSUPPORTED, b"N must be even"),
+    # Any N and any B and C strides are read in place with N-major B (the
+    # checks below reject these calls for other reasons before a launch).
+    (dict(n=61, ldb_k=61, ldc=61, ldb_e=61 * 64, lda=68), nat.MGG_ERR_UNSUPPORTED, b"lda"),
+    # Odd N has kernel instances for 256x256, 128x128 and (N-major 16-bit B,
+    # no fused epilogue) 128x512 tiles only.
+    (dict(n=61, ldb_k=61, ldc=61, ldb_e=61 * 64, bm=64, bn=64), nat.MGG_ERR_UNSUPPORTED, b"odd N"),
+    (dict(n=61, ldb_k=61, ldc=61, ldb_e=61 * 64, bm=256, bn=128), nat.MGG_ERR_UNSUPPORTED,
+     b"odd N"),
+    (dict(dtype=nat.MGG_DTYPE_BF16 | nat.MGG_B_KMAJOR, n=61, ldb_k=64, ldc=61, ldb_e=64 * 61,
+          bm=128, bn=512), nat.MGG_ERR_UNSUPPORTED, b"odd N"),
     (dict(lda=32), nat.MGG_ERR_INVALID, b"leading"),
-    (dict(ldb_k=72, ldb_e=61), nat.MGG_ERR_UNSUPPORTED, b"strides"),
-    (dict(ldb_k=65), nat.MGG_ERR_UNSUPPORTED, b"strides"),
-    (dict(lda=68), nat.MGG_ERR_UNSUPPORTED, b"strides"),
+    (dict(lda=68), nat.MGG_ERR_UNSUPPORTED, b"multiple of 8"),
+    (dict(dtype=nat.MGG_DTYPE_BF16 | nat.MGG_B_KMAJOR, ldb_k=68, ldb_e=68 * 64),
+     nat.MGG_ERR_UNSUPPORTED, b"multiple of 8"),
     (dict(ldc=66, n=60, ldb_k=60, ldb_e=60 * 64, a=FAKE + 8), nat.MGG_ERR_UNSUPPORTED, b"aligned"),
     (dict(a=None), nat.MGG_ERR_INVALID, b"null"),
     (dict(off=None), nat.MGG_ERR_INVALID, b"null"),
