@@ -762,17 +762,22 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       static_assert(BM % 64 == 0 && BN % 64 == 0 && (BM + BN) / 64 <= NW, "one scale DMA per wave");
       if ((int)wave < (BM + BN) / 64) {
         const uint32_t dst = lds_addr(s_scale + iss_scale_buf * (BM + BN) + 64 * wave);
+        // The lane offsets come from an opaque copy of the lane index: kept
+        // live from the kernel's start they were spilled, and their reload
+        // waited for every DMA in flight (vmcnt(0)) once per tile.
+        int ol = lane;
+        asm volatile("" : "+v"(ol));
         if (64 * (int)wave < BM) {
           int64_t rows = p.m - iss.row_base;
           rows = rows < iss.rows_valid ? rows : iss.rows_valid;
           const i32x4 rs = make_rsrc4(p.a_scale + (iss.row_base > 0 ? iss.row_base : 0),
                                       iss.row_base >= 0 && rows > 0 ? rows * 4 : 0);
-          dma4(rs, (uint32_t)(64 * wave + lane) * 4, dst);
+          dma4(rs, (uint32_t)(64 * wave + ol) * 4, dst);
         } else {
           int64_t cols = p.n - iss.n0;
           cols = cols < BN ? cols : BN;
           const i32x4 rs = make_rsrc4(p.b_scale + (int64_t)iss.e * p.n + iss.n0, cols > 0 ? cols * 4 : 0);
-          dma4(rs, (uint32_t)(64 * wave - BM + lane) * 4, dst);
+          dma4(rs, (uint32_t)(64 * wave - BM + ol) * 4, dst);
         }
       }
     }
