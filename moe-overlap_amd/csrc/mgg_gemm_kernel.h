@@ -1006,10 +1006,12 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   constexpr int kWaitEven = kLB == 3 ? kBPerWave + kAPerWave + kBPerWave
                                      : kBPerWave + kBPerWave + kAPerWave + kBPerWave;
   static_assert(!kABlk || (kAPerWave % 2 == 0 && kBPerWave % 2 == 0), "A-block DMA shares come in halves");
-  auto issue_ablock = [&](int m, int t0, int t1) {  // DMAs [t0, t1) of A block m
+  // FULL (a compile-time flag): the caller knows the block or stage lies
+  // wholly inside K, so no DMA of it needs the partial-stage path.
+  auto issue_ablock_f = [&](auto FULL, int m, int t0, int t1) {  // DMAs [t0, t1) of A block m
     const int k0 = m * 2 * kBK;
     const uint32_t la = lds_a0 + (m & 1) * kASlot + wave * kAPerWave * 1024;
-    const bool full = k0 + 2 * kBK <= k_size;
+    const bool full = decltype(FULL)::value != 0 || k0 + 2 * kBK <= k_size;
 #pragma unroll
     for (int t = t0; t < t1; ++t) {
       if (full) {
@@ -1020,10 +1022,10 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       }
     }
   };
-  auto issue_bstage = [&](int st, int d0, int d1) {  // DMAs [d0, d1) of B stage st
+  auto issue_bstage_f = [&](auto FULL, int st, int d0, int d1) {  // DMAs [d0, d1) of B stage st
     const int k0 = st * kBK;
     const uint32_t lb = lds_b0 + (st % kBSlots) * kBStage + wave * kBPerWave * 1024;
-    const bool full = k0 + kBK <= k_size;
+    const bool full = decltype(FULL)::value != 0 || k0 + kBK <= k_size;
 #pragma unroll
     for (int t = d0; t < d1; ++t) {
       if (full) {
@@ -1035,6 +1037,8 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       }
     }
   };
+  auto issue_ablock = [&](int m, int t0, int t1) { issue_ablock_f(IntConst<0>{}, m, t0, t1); };
+  auto issue_bstage = [&](int st, int d0, int d1) { issue_bstage_f(IntConst<0>{}, st, d0, d1); };
   // Half `part` of the fragments of K step kk of stage st (A half H of its block).
   auto read_kstep_ab = [&](auto H, int f, int st, int kk, int part) {
     constexpr int h = decltype(H)::value;
@@ -1050,17 +1054,17 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // on fragment buffer 0 while step 1's fragments are read and this stage's
   // DMAs go out, then step 1, the wait and barrier for stage kt+1, and its
   // first fragments.
-  auto stage_ab = [&](auto H, int kt) {
+  auto stage_ab = [&](auto H, auto FULL, int kt) {
     constexpr int h = decltype(H)::value;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       mfma_group(0, g);
       if (g < 2) read_kstep_ab(H, 1, kt, 1, g);
       if constexpr (h == 0) {
-        if (g < 2) issue_ablock(kt / 2 + 1, g * kAPerWave / 2, (g + 1) * kAPerWave / 2);
-        else issue_bstage(kt + kLB, (g - 2) * kBPerWave / 2, (g - 1) * kBPerWave / 2);
+        if (g < 2) issue_ablock_f(FULL, kt / 2 + 1, g * kAPerWave / 2, (g + 1) * kAPerWave / 2);
+        else issue_bstage_f(FULL, kt + kLB, (g - 2) * kBPerWave / 2, (g - 1) * kBPerWave / 2);
       } else {
-        if (g == 0 || g == 2) issue_bstage(kt + kLB, g / 2 * kBPerWave / 2, (g / 2 + 1) * kBPerWave / 2);
+        if (g == 0 || g == 2) issue_bstage_f(FULL, kt + kLB, g / 2 * kBPerWave / 2, (g / 2 + 1) * kBPerWave / 2);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1105,9 +1109,25 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       read_kstep_ab(IntConst<0>{}, 0, 0, 0, 0);
       read_kstep_ab(IntConst<0>{}, 0, 0, 0, 1);
       const int nk2 = (nk + 1) & ~1;  // pairs of stages; an odd count ends on a zero stage
-      for (int kt = 0; kt < nk2; kt += 2) {
-        stage_ab(IntConst<0>{}, kt);
-        stage_ab(IntConst<1>{}, kt + 1);
+      // Pairs whose issued A block (kt/2 + 1) and B stages (kt + kLB, kt + kLB
+      // + 1) lie wholly inside K run without the partial-stage checks.
+      // (B stage kt + 1 + kLB is full iff (kt + kLB + 2) * kBK <= K; the A block
+      // kt/2 + 1 iff (kt + 4) * kBK <= K.)  A DMA on the full path keeps its
+      // stage offset in the unchecked SGPR offset, so this bound must hold.
+      const int kt_full = k_size / kBK - kLB - 2;  // kt <= kt_full: every issued stage full
+      int kt = 0;
+#ifndef MGG_FULL_LOOP
+#define MGG_FULL_LOOP 1
+#endif
+      if constexpr (MGG_FULL_LOOP) {
+        for (; kt < nk2 && kt <= kt_full; kt += 2) {
+          stage_ab(IntConst<0>{}, IntConst<1>{}, kt);
+          stage_ab(IntConst<1>{}, IntConst<1>{}, kt + 1);
+        }
+      }
+      for (; kt < nk2; kt += 2) {
+        stage_ab(IntConst<0>{}, IntConst<0>{}, kt);
+        stage_ab(IntConst<1>{}, IntConst<0>{}, kt + 1);
       }
       return;
     }
