@@ -51,6 +51,11 @@
 #ifndef MGG_FP8_NW
 #define MGG_FP8_NW 8
 #endif
+// K loops split into stages known to lie wholly inside K (issued without the
+// partial-stage checks) and the rest.
+#ifndef MGG_FULL_LOOP
+#define MGG_FULL_LOOP 1
+#endif
 // Non-temporal B DMAs on the 128x512 tile (kBStream).
 #ifndef MGG_BSTREAM
 #define MGG_BSTREAM 1
@@ -734,12 +739,14 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // and leave L2 to the A lines the expert's other n-tiles read (the
   // reference benchmark's problem: -2.1% striped, -2.9% atomic).
   constexpr bool kBStream = MGG_BSTREAM && BN == 512 && !T::kBKMajor;
-  auto issue_part = [&](int s, int d0, int d1) {
+  // FULL (a compile-time flag): the caller knows stage s lies wholly inside
+  // K, so no DMA of it needs the partial-stage path.
+  auto issue_part_f = [&](auto FULL, int s, int d0, int d1) {
     const int k0 = s * kBK;
     const int buf = s % kStages;
     const uint32_t la = lds_a0 + buf * kAStage + wave * kAPerWave * 1024;
     const uint32_t lb = lds_b0 + buf * kBStage + wave * kBPerWave * 1024;
-    const bool full = k0 + kBK <= k_size;
+    const bool full = decltype(FULL)::value != 0 || k0 + kBK <= k_size;
 #pragma unroll
     for (int d = d0; d < d1; ++d) {
       if (d < kAPerWave) {
@@ -773,6 +780,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       }
     }
   };
+  auto issue_part = [&](int s, int d0, int d1) { issue_part_f(IntConst<0>{}, s, d0, d1); };
   // Scaled types: the tile's BM row scales and BN column scales go to its LDS
   // scale buffer by DMA with its stage 0 (one 64-word DMA per wave for the
   // first (BM+BN)/64 waves), so the first stage wait covers them; rows past
@@ -927,12 +935,12 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // fragment buffer of the stage's first K step, a compile-time constant.
   int issued = -1;
   constexpr int kEarlyGroups = kSteps > 1 ? 4 * (kSteps - 1) : 1;
-  auto dma_share = [&](int grp, int s) {
+  auto dma_share = [&](auto FULL, int grp, int s) {
     const int d0 = grp * kDmaPerStage / kEarlyGroups;
     const int d1 = (grp + 1) * kDmaPerStage / kEarlyGroups;
-    if (d1 > d0) issue_part(s, d0, d1);
+    if (d1 > d0) issue_part_f(FULL, s, d0, d1);
   };
-  auto early_steps = [&](auto P0, int buf, int next_stage, bool issue) {
+  auto early_steps = [&](auto P0, auto FULL, int buf, int next_stage, bool issue) {
     constexpr int p0 = decltype(P0)::value;
 #pragma unroll
     for (int kk = 0; kk + 1 < kSteps; ++kk) {
@@ -941,28 +949,34 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
         mfma_group((p0 + kk) & 1, g);
         if constexpr (kASingle) read_a(0, buf, kk + 1, g);
         if (g < 2) read_kstep((p0 + kk + 1) & 1, buf, kk + 1, g);
-        if (issue) dma_share(kk * 4 + g, next_stage);
+        if (decltype(FULL)::value != 0 || issue) dma_share(FULL, kk * 4 + g, next_stage);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
-  // A stage that has a successor to publish.
-  auto stage = [&](auto P0, int kt) {
+  // A stage that has a successor to publish.  FULL: the stage it issues,
+  // kt+kStages-1, lies wholly inside K (so it is issued, and its wait counts
+  // kStages-2 stages issued after kt+1).
+  auto stage = [&](auto P0, auto FULL, int kt) {
     constexpr int p0 = decltype(P0)::value;
+    constexpr bool full = decltype(FULL)::value != 0;
     constexpr int f_last = (p0 + kSteps - 1) & 1;
     constexpr int f_next = (p0 + kSteps) & 1;
     const int buf = kt % kStages;
     // Stage kt+kStages-1 goes into the buffer stage kt-1 used; every wave
     // finished reading it before the barrier of stage kt-1.
-    const bool issue = kt + kStages - 1 < nk;
+    const bool issue = full || kt + kStages - 1 < nk;
     if (issue) issued = kt + kStages - 1;
     if constexpr (kSteps == 1) {
-      if (issue) issue_stage(kt + kStages - 1);
+      if (issue) issue_part_f(FULL, kt + kStages - 1, 0, kDmaPerStage);
     }
-    early_steps(P0, buf, kt + kStages - 1, issue);
+    early_steps(P0, FULL, buf, kt + kStages - 1, issue);
     mfma_group(f_last, 0);
     __builtin_amdgcn_sched_barrier(0);
-    wait_stage(kt + 1, issued);
+    if constexpr (full)
+      wait_dma<(kStages - 2) * kDmaPerStage>();
+    else
+      wait_stage(kt + 1, issued);
     __syncthreads();
     const int nbuf = (kt + 1) % kStages;
     if constexpr (kASingle) read_a(0, nbuf, 0, 0);
@@ -980,7 +994,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   };
   auto last_stage = [&](auto P0, int kt) {
     constexpr int p0 = decltype(P0)::value;
-    early_steps(P0, kt % kStages, 0, false);
+    early_steps(P0, IntConst<0>{}, kt % kStages, 0, false);
 #pragma unroll
     for (int g = 0; g < 4; ++g) mfma_group((p0 + kSteps - 1) & 1, g);
   };
@@ -1116,9 +1130,6 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       // stage offset in the unchecked SGPR offset, so this bound must hold.
       const int kt_full = k_size / kBK - kLB - 2;  // kt <= kt_full: every issued stage full
       int kt = 0;
-#ifndef MGG_FULL_LOOP
-#define MGG_FULL_LOOP 1
-#endif
       if constexpr (MGG_FULL_LOOP) {
         for (; kt < nk2 && kt <= kt_full; kt += 2) {
           stage_ab(IntConst<0>{}, IntConst<1>{}, kt);
@@ -1136,16 +1147,28 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       read_kstep(0, 0, 0, 1, 1);
     }
     int kt = 0;
+    // Stages whose issued stage kt+kStages-1 lies wholly inside K run without
+    // the partial-stage checks: kt <= kt_full.  (A DMA on the full path keeps
+    // its stage offset in the unchecked SGPR offset, so this bound must hold.)
+    const int kt_full = k_size / kBK - kStages;
     if constexpr (kSteps % 2 == 0) {  // every stage starts on fragment buffer 0
-      for (; kt + 1 < nk; ++kt) stage(IntConst<0>{}, kt);
+      if constexpr (MGG_FULL_LOOP)
+        for (; kt + 1 < nk && kt <= kt_full; ++kt) stage(IntConst<0>{}, IntConst<1>{}, kt);
+      for (; kt + 1 < nk; ++kt) stage(IntConst<0>{}, IntConst<0>{}, kt);
       if (nk > 0) last_stage(IntConst<0>{}, kt);
     } else {  // one-step stages alternate buffers: unrolled by two
+      if constexpr (MGG_FULL_LOOP) {
+        for (; kt + 2 < nk && kt + 1 <= kt_full; kt += 2) {
+          stage(IntConst<0>{}, IntConst<1>{}, kt);
+          stage(IntConst<1>{}, IntConst<1>{}, kt + 1);
+        }
+      }
       for (; kt + 2 < nk; kt += 2) {
-        stage(IntConst<0>{}, kt);
-        stage(IntConst<1>{}, kt + 1);
+        stage(IntConst<0>{}, IntConst<0>{}, kt);
+        stage(IntConst<1>{}, IntConst<0>{}, kt + 1);
       }
       if (kt + 1 < nk) {
-        stage(IntConst<0>{}, kt);
+        stage(IntConst<0>{}, IntConst<0>{}, kt);
         last_stage(IntConst<1>{}, kt + 1);
       } else if (nk > 0) {
         last_stage(IntConst<0>{}, kt);
