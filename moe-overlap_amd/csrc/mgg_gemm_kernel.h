@@ -161,6 +161,15 @@ struct IntConst {
   static constexpr int value = V;
 };
 
+// f(IntConst<0>{}), ..., f(IntConst<N-1>{}) in order.
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(IntConst<I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
 // Fused epilogues (element-wise on the fp32 accumulator, before rounding to
 // 16 bits).  They run on 128 values per lane per tile while the matrix cores
 // wait, so they use the hardware reciprocal and base-2 exponential (about
@@ -741,9 +750,10 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   constexpr bool kBStream = MGG_BSTREAM && BN == 512 && !T::kBKMajor;
   // FULL (a compile-time flag): the caller knows stage s lies wholly inside
   // K, so no DMA of it needs the partial-stage path.
-  auto issue_part_f = [&](auto FULL, int s, int d0, int d1) {
+  // buf: the LDS buffer of stage s (s % kStages), a constant where the
+  // caller knows it.
+  auto issue_part_f = [&](auto FULL, int s, int d0, int d1, int buf) {
     const int k0 = s * kBK;
-    const int buf = s % kStages;
     const uint32_t la = lds_a0 + buf * kAStage + wave * kAPerWave * 1024;
     const uint32_t lb = lds_b0 + buf * kBStage + wave * kBPerWave * 1024;
     const bool full = decltype(FULL)::value != 0 || k0 + kBK <= k_size;
@@ -780,7 +790,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       }
     }
   };
-  auto issue_part = [&](int s, int d0, int d1) { issue_part_f(IntConst<0>{}, s, d0, d1); };
+  auto issue_part = [&](int s, int d0, int d1) { issue_part_f(IntConst<0>{}, s, d0, d1, s % kStages); };
   // Scaled types: the tile's BM row scales and BN column scales go to its LDS
   // scale buffer by DMA with its stage 0 (one 64-word DMA per wave for the
   // first (BM+BN)/64 waves), so the first stage wait covers them; rows past
@@ -935,12 +945,12 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // fragment buffer of the stage's first K step, a compile-time constant.
   int issued = -1;
   constexpr int kEarlyGroups = kSteps > 1 ? 4 * (kSteps - 1) : 1;
-  auto dma_share = [&](auto FULL, int grp, int s) {
+  auto dma_share = [&](auto FULL, int grp, int s, int sbuf) {
     const int d0 = grp * kDmaPerStage / kEarlyGroups;
     const int d1 = (grp + 1) * kDmaPerStage / kEarlyGroups;
-    if (d1 > d0) issue_part_f(FULL, s, d0, d1);
+    if (d1 > d0) issue_part_f(FULL, s, d0, d1, sbuf);
   };
-  auto early_steps = [&](auto P0, auto FULL, int buf, int next_stage, bool issue) {
+  auto early_steps = [&](auto P0, auto FULL, int buf, int next_stage, int next_buf, bool issue) {
     constexpr int p0 = decltype(P0)::value;
 #pragma unroll
     for (int kk = 0; kk + 1 < kSteps; ++kk) {
@@ -949,28 +959,31 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
         mfma_group((p0 + kk) & 1, g);
         if constexpr (kASingle) read_a(0, buf, kk + 1, g);
         if (g < 2) read_kstep((p0 + kk + 1) & 1, buf, kk + 1, g);
-        if (decltype(FULL)::value != 0 || issue) dma_share(FULL, kk * 4 + g, next_stage);
+        if (decltype(FULL)::value != 0 || issue) dma_share(FULL, kk * 4 + g, next_stage, next_buf);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
   // A stage that has a successor to publish.  FULL: the stage it issues,
   // kt+kStages-1, lies wholly inside K (so it is issued, and its wait counts
-  // kStages-2 stages issued after kt+1).
-  auto stage = [&](auto P0, auto FULL, int kt) {
+  // kStages-2 stages issued after kt+1).  BUFC: kt % kStages when the caller
+  // knows it at compile time (else -1), so LDS addresses fold to constants.
+  auto stage = [&](auto P0, auto FULL, auto BUFC, int kt) {
     constexpr int p0 = decltype(P0)::value;
     constexpr bool full = decltype(FULL)::value != 0;
+    constexpr int bc = decltype(BUFC)::value;
     constexpr int f_last = (p0 + kSteps - 1) & 1;
     constexpr int f_next = (p0 + kSteps) & 1;
-    const int buf = kt % kStages;
+    const int buf = bc >= 0 ? bc : kt % kStages;
     // Stage kt+kStages-1 goes into the buffer stage kt-1 used; every wave
     // finished reading it before the barrier of stage kt-1.
+    const int ibuf = bc >= 0 ? (bc + kStages - 1) % kStages : (kt + kStages - 1) % kStages;
     const bool issue = full || kt + kStages - 1 < nk;
     if (issue) issued = kt + kStages - 1;
     if constexpr (kSteps == 1) {
-      if (issue) issue_part_f(FULL, kt + kStages - 1, 0, kDmaPerStage);
+      if (issue) issue_part_f(FULL, kt + kStages - 1, 0, kDmaPerStage, ibuf);
     }
-    early_steps(P0, FULL, buf, kt + kStages - 1, issue);
+    early_steps(P0, FULL, buf, kt + kStages - 1, ibuf, issue);
     mfma_group(f_last, 0);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (full)
@@ -978,7 +991,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     else
       wait_stage(kt + 1, issued);
     __syncthreads();
-    const int nbuf = (kt + 1) % kStages;
+    const int nbuf = bc >= 0 ? (bc + 1) % kStages : (kt + 1) % kStages;
     if constexpr (kASingle) read_a(0, nbuf, 0, 0);
     mfma_group(f_last, 1);
     if constexpr (kASingle) read_a(0, nbuf, 0, 1);
@@ -994,7 +1007,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   };
   auto last_stage = [&](auto P0, int kt) {
     constexpr int p0 = decltype(P0)::value;
-    early_steps(P0, IntConst<0>{}, kt % kStages, 0, false);
+    early_steps(P0, IntConst<0>{}, kt % kStages, 0, 0, false);
 #pragma unroll
     for (int g = 0; g < 4; ++g) mfma_group((p0 + kSteps - 1) & 1, g);
   };
@@ -1152,23 +1165,28 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     // its stage offset in the unchecked SGPR offset, so this bound must hold.)
     const int kt_full = k_size / kBK - kStages;
     if constexpr (kSteps % 2 == 0) {  // every stage starts on fragment buffer 0
-      if constexpr (MGG_FULL_LOOP)
-        for (; kt + 1 < nk && kt <= kt_full; ++kt) stage(IntConst<0>{}, IntConst<1>{}, kt);
-      for (; kt + 1 < nk; ++kt) stage(IntConst<0>{}, IntConst<0>{}, kt);
+      if constexpr (MGG_FULL_LOOP) {
+        // Full stages unrolled by the ring length from kt = 0, so each
+        // stage's LDS buffer is a compile-time constant.
+        for (; kt + kStages < nk && kt + kStages - 1 <= kt_full; kt += kStages)
+          static_for<kStages>([&](auto B) { stage(IntConst<0>{}, IntConst<1>{}, B, kt + decltype(B)::value); });
+        for (; kt + 1 < nk && kt <= kt_full; ++kt) stage(IntConst<0>{}, IntConst<1>{}, IntConst<-1>{}, kt);
+      }
+      for (; kt + 1 < nk; ++kt) stage(IntConst<0>{}, IntConst<0>{}, IntConst<-1>{}, kt);
       if (nk > 0) last_stage(IntConst<0>{}, kt);
     } else {  // one-step stages alternate buffers: unrolled by two
       if constexpr (MGG_FULL_LOOP) {
         for (; kt + 2 < nk && kt + 1 <= kt_full; kt += 2) {
-          stage(IntConst<0>{}, IntConst<1>{}, kt);
-          stage(IntConst<1>{}, IntConst<1>{}, kt + 1);
+          stage(IntConst<0>{}, IntConst<1>{}, IntConst<-1>{}, kt);
+          stage(IntConst<1>{}, IntConst<1>{}, IntConst<-1>{}, kt + 1);
         }
       }
       for (; kt + 2 < nk; kt += 2) {
-        stage(IntConst<0>{}, IntConst<0>{}, kt);
-        stage(IntConst<1>{}, IntConst<0>{}, kt + 1);
+        stage(IntConst<0>{}, IntConst<0>{}, IntConst<-1>{}, kt);
+        stage(IntConst<1>{}, IntConst<0>{}, IntConst<-1>{}, kt + 1);
       }
       if (kt + 1 < nk) {
-        stage(IntConst<0>{}, IntConst<0>{}, kt);
+        stage(IntConst<0>{}, IntConst<0>{}, IntConst<-1>{}, kt);
         last_stage(IntConst<1>{}, kt + 1);
       } else if (nk > 0) {
         last_stage(IntConst<0>{}, kt);
