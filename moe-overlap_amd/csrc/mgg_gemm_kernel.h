@@ -1035,9 +1035,11 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   static_assert(!kABlk || (kAPerWave % 2 == 0 && kBPerWave % 2 == 0), "A-block DMA shares come in halves");
   // FULL (a compile-time flag): the caller knows the block or stage lies
   // wholly inside K, so no DMA of it needs the partial-stage path.
-  auto issue_ablock_f = [&](auto FULL, int m, int t0, int t1) {  // DMAs [t0, t1) of A block m
+  // aslot / bslot: the LDS slot (m & 1, st % kBSlots), constants where the
+  // caller knows them.
+  auto issue_ablock_f = [&](auto FULL, int m, int t0, int t1, int aslot) {  // DMAs [t0, t1) of A block m
     const int k0 = m * 2 * kBK;
-    const uint32_t la = lds_a0 + (m & 1) * kASlot + wave * kAPerWave * 1024;
+    const uint32_t la = lds_a0 + aslot * kASlot + wave * kAPerWave * 1024;
     const bool full = decltype(FULL)::value != 0 || k0 + 2 * kBK <= k_size;
 #pragma unroll
     for (int t = t0; t < t1; ++t) {
@@ -1049,9 +1051,9 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       }
     }
   };
-  auto issue_bstage_f = [&](auto FULL, int st, int d0, int d1) {  // DMAs [d0, d1) of B stage st
+  auto issue_bstage_f = [&](auto FULL, int st, int d0, int d1, int bslot) {  // DMAs [d0, d1) of B stage st
     const int k0 = st * kBK;
-    const uint32_t lb = lds_b0 + (st % kBSlots) * kBStage + wave * kBPerWave * 1024;
+    const uint32_t lb = lds_b0 + bslot * kBStage + wave * kBPerWave * 1024;
     const bool full = decltype(FULL)::value != 0 || k0 + kBK <= k_size;
 #pragma unroll
     for (int t = d0; t < d1; ++t) {
@@ -1064,34 +1066,44 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       }
     }
   };
-  auto issue_ablock = [&](int m, int t0, int t1) { issue_ablock_f(IntConst<0>{}, m, t0, t1); };
-  auto issue_bstage = [&](int st, int d0, int d1) { issue_bstage_f(IntConst<0>{}, st, d0, d1); };
-  // Half `part` of the fragments of K step kk of stage st (A half H of its block).
-  auto read_kstep_ab = [&](auto H, int f, int st, int kk, int part) {
+  auto issue_ablock = [&](int m, int t0, int t1) { issue_ablock_f(IntConst<0>{}, m, t0, t1, m & 1); };
+  auto issue_bstage = [&](int st, int d0, int d1) {
+    issue_bstage_f(IntConst<0>{}, st, d0, d1, st % kBSlots);
+  };
+  // Half `part` of the fragments of K step kk of stage st (A half H of its
+  // block); q: st % 4 when the caller knows it at compile time (else -1).
+  auto read_kstep_ab = [&](auto H, int f, int st, int kk, int part, int q = -1) {
     constexpr int h = decltype(H)::value;
-    const int aslot = (st >> 1) & 1;
+    const int aslot = q >= 0 ? (q >> 1) & 1 : (st >> 1) & 1;
+    const int bslot = q >= 0 && kBSlots == 4 ? q : st % kBSlots;
 #pragma unroll
     for (int j = part * kMB / 2; j < (part + 1) * kMB / 2; ++j)
       fa[f][j] = read_rows(a_off[kABlk ? h : 0][kk], aslot * kASlot + 32 * kALdsRow * j);
 #pragma unroll
     for (int i = part * kNB / 2; i < (part + 1) * kNB / 2 + (kNB == 1 && part == 0); ++i)
-      read_b(f, st % kBSlots, kk, i);
+      read_b(f, bslot, kk, i);
   };
   // Stage kt of A half H (kt % 2 == H), in run_worker's stage order: K step 0
   // on fragment buffer 0 while step 1's fragments are read and this stage's
   // DMAs go out, then step 1, the wait and barrier for stage kt+1, and its
   // first fragments.
-  auto stage_ab = [&](auto H, auto FULL, int kt) {
+  // Q: kt % 4 when the caller knows it at compile time (else -1), so the LDS
+  // slots fold to constants.
+  auto stage_ab = [&](auto H, auto FULL, auto Q, int kt) {
     constexpr int h = decltype(H)::value;
+    constexpr int q = decltype(Q)::value;
+    const int aslot_next = q >= 0 ? ((q >> 1) + 1) & 1 : (kt / 2 + 1) & 1;
+    const int bslot_next = q >= 0 && kBSlots == 4 ? (q + kLB) % 4 : (kt + kLB) % kBSlots;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       mfma_group(0, g);
-      if (g < 2) read_kstep_ab(H, 1, kt, 1, g);
+      if (g < 2) read_kstep_ab(H, 1, kt, 1, g, q);
       if constexpr (h == 0) {
-        if (g < 2) issue_ablock_f(FULL, kt / 2 + 1, g * kAPerWave / 2, (g + 1) * kAPerWave / 2);
-        else issue_bstage_f(FULL, kt + kLB, (g - 2) * kBPerWave / 2, (g - 1) * kBPerWave / 2);
+        if (g < 2) issue_ablock_f(FULL, kt / 2 + 1, g * kAPerWave / 2, (g + 1) * kAPerWave / 2, aslot_next);
+        else issue_bstage_f(FULL, kt + kLB, (g - 2) * kBPerWave / 2, (g - 1) * kBPerWave / 2, bslot_next);
       } else {
-        if (g == 0 || g == 2) issue_bstage_f(FULL, kt + kLB, g / 2 * kBPerWave / 2, (g / 2 + 1) * kBPerWave / 2);
+        if (g == 0 || g == 2)
+          issue_bstage_f(FULL, kt + kLB, g / 2 * kBPerWave / 2, (g / 2 + 1) * kBPerWave / 2, bslot_next);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1100,10 +1112,10 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     wait_dma<h == 0 ? kWaitEven : kWaitOdd>();
     __syncthreads();
     mfma_group(1, 1);
-    read_kstep_ab(IntConst<1 - h>{}, 0, kt + 1, 0, 0);
+    read_kstep_ab(IntConst<1 - h>{}, 0, kt + 1, 0, 0, q >= 0 ? (q + 1) % 4 : -1);
     __builtin_amdgcn_sched_barrier(0);
     mfma_group(1, 2);
-    read_kstep_ab(IntConst<1 - h>{}, 0, kt + 1, 0, 1);
+    read_kstep_ab(IntConst<1 - h>{}, 0, kt + 1, 0, 1, q >= 0 ? (q + 1) % 4 : -1);
     __builtin_amdgcn_sched_barrier(0);
     mfma_group(1, 3);
     __builtin_amdgcn_sched_barrier(0);
@@ -1144,14 +1156,21 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       const int kt_full = k_size / kBK - kLB - 2;  // kt <= kt_full: every issued stage full
       int kt = 0;
       if constexpr (MGG_FULL_LOOP) {
+        // Two pairs per iteration from kt = 0 (kt % 4 known: constant slots).
+        for (; kt + 2 < nk2 && kt + 2 <= kt_full; kt += 4) {
+          stage_ab(IntConst<0>{}, IntConst<1>{}, IntConst<0>{}, kt);
+          stage_ab(IntConst<1>{}, IntConst<1>{}, IntConst<1>{}, kt + 1);
+          stage_ab(IntConst<0>{}, IntConst<1>{}, IntConst<2>{}, kt + 2);
+          stage_ab(IntConst<1>{}, IntConst<1>{}, IntConst<3>{}, kt + 3);
+        }
         for (; kt < nk2 && kt <= kt_full; kt += 2) {
-          stage_ab(IntConst<0>{}, IntConst<1>{}, kt);
-          stage_ab(IntConst<1>{}, IntConst<1>{}, kt + 1);
+          stage_ab(IntConst<0>{}, IntConst<1>{}, IntConst<-1>{}, kt);
+          stage_ab(IntConst<1>{}, IntConst<1>{}, IntConst<-1>{}, kt + 1);
         }
       }
       for (; kt < nk2; kt += 2) {
-        stage_ab(IntConst<0>{}, IntConst<0>{}, kt);
-        stage_ab(IntConst<1>{}, IntConst<0>{}, kt + 1);
+        stage_ab(IntConst<0>{}, IntConst<0>{}, IntConst<-1>{}, kt);
+        stage_ab(IntConst<1>{}, IntConst<0>{}, IntConst<-1>{}, kt + 1);
       }
       return;
     }
