@@ -104,6 +104,10 @@ def parse_args():
     p.add_argument("--profile-only", action="store_true",
                    help="only the warmup, settle and timed steps (for rocprofv3 runs)")
     p.add_argument("--no-settle", action="store_true", help="skip the clock-settling phase")
+    p.add_argument("--vendor-bmm", action="store_true",
+                   help="with --profile-only and equal counts: run hipBLASLt's batched GEMM "
+                        "(torch.bmm) on the same operands instead of the grouped GEMM, for "
+                        "counter comparisons (analysis only)")
     # The benchmark's operands are random; the others keep every byte moved and every MFMA
     # issued but change the data, which shows how the card's power limit sets its clock.
     p.add_argument("--operands", default="random", choices=["random", "zero_a", "zero_b", "constant"],
@@ -683,6 +687,16 @@ def main():
 
     def step():
         return gg.persistent_grouped_gemm(case.a, case.b, offs, **kw)
+
+    if args.vendor_bmm:
+        counts_l = case.counts.tolist()
+        if not args.profile_only or len(set(counts_l)) != 1 or counts_l[0] <= 0:
+            print("--vendor-bmm needs --profile-only and equal, non-zero counts", file=sys.stderr)
+            sys.exit(2)
+        a3 = case.a.view(case.num_experts, counts_l[0], case.k)
+
+        def step():  # noqa: F811 (the vendor library's kernel on the same operands)
+            return torch.bmm(a3, case.b)
 
     flops = case.flops
     nbytes = case.algorithmic_bytes()
