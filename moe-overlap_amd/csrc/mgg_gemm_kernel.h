@@ -56,6 +56,10 @@
 #ifndef MGG_FULL_LOOP
 #define MGG_FULL_LOOP 1
 #endif
+// Atomic schedule: the rounds before the last by the striped placement.
+#ifndef MGG_STATIC_ROUNDS
+#define MGG_STATIC_ROUNDS 1
+#endif
 // Non-temporal B DMAs on the 128x512 tile (kBStream).
 #ifndef MGG_BSTREAM
 #define MGG_BSTREAM 1
@@ -205,17 +209,19 @@ __device__ __forceinline__ float silu_mul(float gate, float up) {  // silu(gate)
 template <int BM, int NT>
 __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_prefix,
                                  int32_t* s_offs, int32_t* s_scan, int rep_tiles,
-                                 int32_t* w_report) {
+                                 int32_t* w_report, bool* whole_m_tiles) {
   const int tid = threadIdx.x;
   const int E = p.num_experts;
   const int per = (E + NT - 1) / NT;
   const int e0 = tid * per;
   int32_t local = 0;
   int64_t rep_local = 0;
+  int partial = 0;  // an expert whose last m-tile is partial
   for (int i = 0; i < per; ++i) {
     const int e = e0 + i;
     if (e < E) {
       const int64_t cnt = (int64_t)p.offsets[e + 1] - (int64_t)p.offsets[e];
+      partial |= cnt > 0 && cnt % BM != 0;
       const int64_t tiles = cnt > 0 ? ((cnt + BM - 1) / BM) * (int64_t)n_tiles : 0;
       local += (int32_t)tiles;
       if (rep_tiles > 0 && cnt > 0) rep_local += ((cnt + p.report_bm - 1) / p.report_bm) * (int64_t)rep_tiles;
@@ -260,7 +266,7 @@ __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_pr
     s_prefix[E] = incl;
     if (s_offs != nullptr) s_offs[E] = p.offsets[E];
   }
-  __syncthreads();
+  *whole_m_tiles = __syncthreads_or(partial) == 0;
   const int32_t W = s_prefix[E];
   if (rep_tiles <= 0) *w_report = W;
   return W;
@@ -449,7 +455,8 @@ constexpr bool ablk_mode() {
 // current one.  `first` is this worker's first item (a ticket in atomic mode).
 template <int BM, int BN, int SBK, int NSTAGE, int NW, class T, int EPI>
 __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles, int32_t w_report,
-                                           int32_t first, int n_tiles, const int32_t* s_prefix,
+                                           bool whole_m_tiles, int32_t first, int n_tiles,
+                                           const int32_t* s_prefix,
                                            const int32_t* s_offs, int32_t* s_item, uint8_t* lds,
                                            float* s_scale) {
   constexpr int kBK = SBK;                  // K (elements) per stage
@@ -525,24 +532,57 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
       W = w_base + rem * split_s;
     }
   }
-  // Atomic schedule: tickets 0 .. W-1 are drawn in all.  Items past the
-  // first G take one ticket each (W - G of them when W > G) and every worker
-  // with a first item (min(W, G) of them) draws one ticket past the queue
-  // before it stops, so the worker that draws ticket W-1 is the last to touch
-  // the counter: it tags the word with the next launch's epoch and hands the
-  // caller's work_counter the value the reference's counter ends at (W + G,
-  // for the report tile's queue length).  Drawn by lane 0 only, in two
-  // halves: the atomic add is issued inside a tile's K loop and its value is
-  // looked at only once the tile's K loop is done (a branch on it inside the
-  // loop would make the wave wait for every DMA it has in flight).
+  // Atomic schedule: a worker's first S items are its stripes (items v, v+G,
+  // ..., in the striped schedule's XCD-aware placement, no ticket), the rest
+  // go by tickets t of the global counter, standing for items S*G + t.  When
+  // every expert's rows fill whole m-tiles (all tiles cost alike, so the
+  // striped placement is balanced) and the queue is derived on the device, S
+  // is the number of whole rounds less one (at least 1): the rounds before
+  // the last keep each XCD's L2 sharing an expert's A and B blocks, and the
+  // last round and the split tail absorb what is uneven.  Otherwise S = 1.
+  // Items past S*G take one ticket each (W - S*G of them when W > S*G) and
+  // every worker with a first item (min(W, G) of them) draws one ticket past
+  // the queue before it stops, so the worker that draws the last ticket,
+  // W - S*G + G - 1 (W - 1 when W <= G), is the last to touch the counter:
+  // it tags the word with the next launch's epoch and hands the caller's
+  // work_counter the value the reference's counter ends at (W + G, for the
+  // report tile's queue length).  Drawn by lane 0 only, in two halves: the
+  // atomic add is issued inside a tile's K loop and its value is looked at
+  // only once the tile's K loop is done (a branch on it inside the loop would
+  // make the wave wait for every DMA it has in flight).
+  // (Not on the fp8 256x256 tile: it sits at the register limit, and the
+  // bookkeeping made it spill more for no gain there.)
+  constexpr bool kStaticRounds = MGG_STATIC_ROUNDS && !(T::kScaled && BM == 256 && BN == 256);
+  // (dyn_base = S * G, recomputed where used: every value kept live through
+  // the kernel costs registers the K loop needs.)
+  auto dyn_base = [&]() -> int32_t {
+    if constexpr (kStaticRounds)
+      if (p.atomic && p.num_work < 0 && whole_m_tiles && W_tiles >= 2 * G) return (W_tiles / G - 1) * G;
+    return G;
+  };
+  // Whether the item after `item` is drawn by ticket (else it is item + G):
+  // a worker's stripes are below dyn_base, drawn items at or above it.
+  auto by_ticket_after = [&](int32_t item) -> bool {
+    if constexpr (!kStaticRounds) return p.atomic != 0;
+    return p.atomic && item + G >= dyn_base();
+  };
   auto resolve = [&](unsigned long long raw) -> int32_t {
     const int32_t t = ticket_from(raw, p.counter, p.epoch);
-    if (t == W - 1) {
-      __hip_atomic_store(p.counter, (unsigned long long)p.next_epoch << 32, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-      if (p.report != nullptr) atomicExch(p.report, w_report + G);
+    if constexpr (kStaticRounds) {
+      if (t == (W > G ? W - dyn_base() + G - 1 : W - 1)) {
+        __hip_atomic_store(p.counter, (unsigned long long)p.next_epoch << 32, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        if (p.report != nullptr) atomicExch(p.report, w_report + G);
+      }
+      return dyn_base() + t;
+    } else {
+      if (t == W - 1) {
+        __hip_atomic_store(p.counter, (unsigned long long)p.next_epoch << 32, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        if (p.report != nullptr) atomicExch(p.report, w_report + G);
+      }
+      return G + t;
     }
-    return G + t;
   };
   auto draw = [&]() -> int32_t { return resolve(atomicAdd(p.counter, 1ull)); };
   // K < 2^30 (the host bounds (K+8)*ldb_k*2 below 2^31), so stage positions
@@ -1545,7 +1585,10 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     __syncthreads();
     return t;
   };
-  auto advance = [&](int32_t item) -> int32_t { return p.atomic ? take_ticket_now() : item + G; };
+  auto advance = [&](int32_t item) -> int32_t {
+    if constexpr (!kStaticRounds) return p.atomic ? take_ticket_now() : item + G;
+    return by_ticket_after(item) ? take_ticket_now() : item + G;
+  };
   // The first valid item at or after `item` (W or more when none is left).
   auto find_valid = [&](int32_t item, Coords& c) -> int32_t {
     while ((uint32_t)item < (uint32_t)W && !decode(item, c)) item = advance(item);
@@ -1569,11 +1612,12 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   }
   for (;;) {
     unsigned long long ticket = 0;
-    main_loop(p.atomic != 0, ticket);
+    main_loop(kStaticRounds ? by_ticket_after(w) : p.atomic != 0, ticket);
     // The next item: the ticket taken during this tile, or the next stripe.
-    if (p.atomic && tid == 0) *s_item = resolve(ticket);
+    // (Recomputed rather than kept live across the K loop.)
+    if ((kStaticRounds ? by_ticket_after(w) : p.atomic != 0) && tid == 0) *s_item = resolve(ticket);
     __syncthreads();  // every wave is done reading this tile's LDS stages; s_item is visible
-    int32_t next = p.atomic ? *s_item : w + G;
+    int32_t next = (kStaticRounds ? by_ticket_after(w) : p.atomic != 0) ? *s_item : w + G;
     // A split part meets the others before anything of the next item is
     // issued (fewer registers live across the meetings).
     const bool store_cur = cur.slot < 0 || split_fixup(cur);
@@ -1674,12 +1718,13 @@ grouped_gemm_kernel(GemmParams p) {
   const int rep_tiles = rep_other ? (int)((p.n + p.report_bn - 1) / p.report_bn) : 0;
   int32_t w_report = 0;
   int32_t W;
+  bool whole_m_tiles = false;  // every expert's rows fill whole m-tiles: equal-cost tiles
   if (p.num_work >= 0) {
     W = p.num_work;
     w_report = rep_other ? queue_length<NT>(p, p.report_bm, rep_tiles, s_scan) : W;
   } else {
     W = derive_prefix<BM, NT>(p, n_tiles, s_prefix, kOffsLds ? s_offs : nullptr, s_scan,
-                              rep_tiles, &w_report);
+                              rep_tiles, &w_report, &whole_m_tiles);
   }
   if (W == 0) {
     // No ticket is drawn: the counter word is handed on to the next launch
@@ -1702,7 +1747,7 @@ grouped_gemm_kernel(GemmParams p) {
   // XCD-aware placement), then tickets t of the global counter stand for
   // items G + t; a worker stops at its first ticket past the queue.
   const int32_t first = v;
-  run_worker<BM, BN, SBK, NSTAGE, NW, T, EPI>(p, W, w_report, first, n_tiles, s_prefix,
+  run_worker<BM, BN, SBK, NSTAGE, NW, T, EPI>(p, W, w_report, whole_m_tiles, first, n_tiles, s_prefix,
                                          (kOffsLds && p.num_work < 0) ? s_offs : nullptr,
                                          s_item, lds, s_scale);
   if (probe) {
