@@ -150,7 +150,10 @@ int mgg_build_work_queue_host(const int64_t* expert_offsets, int64_t num_experts
  * use_atomic_queue = 0: worker w takes items w, w+G, w+2G, ... (workers are
  * numbered so that each XCD owns a contiguous slice of every round).
  * use_atomic_queue = 1: workers take the next item with an atomic add on a
- * 64-bit counter word owned by the library: one per (device, stream) for
+ * 64-bit counter word (every worker's first item, and with the
+ * device-derived queue and counts that fill whole block_m-row tiles its
+ * items of every round but the last, are its stripes, taken without a
+ * ticket).  The word is owned by the library: one per (device, stream) for
  * direct launches, and one per (capture, stream) for launches captured into
  * a HIP graph (so graph replays never share a word with other launches; the
  * word is released when the graph is destroyed).  The words live in a
@@ -303,8 +306,9 @@ int mgg_debug_set_split_flags(uint64_t value, void* stream);
 /*
  * The atomic schedule's split last round, no counterpart in the reference
  * (its atomic kernel takes whole items).  With the device-derived queue, an
- * atomic launch whose last round holds at most a quarter (a half) as many
- * tiles as workers takes each of those tiles as 4 (2) parts of K; the parts'
+ * atomic launch whose last round holds at most a quarter (a third, a half)
+ * as many tiles as workers takes each of those tiles as 4 (3, 2) parts of K
+ * (each part at least two stages); the parts'
  * fp32 sums meet in a per-(device, stream) workspace of one 256 x 256 fp32
  * slot per CU (64 MiB on a 256-CU device) plus one flag word per CU.  The
  * sums then round differently in the last bits from the unsplit tile
