@@ -56,7 +56,8 @@
 #ifndef MGG_FULL_LOOP
 #define MGG_FULL_LOOP 1
 #endif
-// Atomic schedule: the rounds before the last by the striped placement.
+// Atomic schedule on equal-cost tiles: whole rounds by the striped placement
+// (all rounds when the tiles make whole rounds, else all but the last).
 #ifndef MGG_STATIC_ROUNDS
 #define MGG_STATIC_ROUNDS 1
 #endif
@@ -539,7 +540,9 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // striped placement is balanced) and the queue is derived on the device, S
   // is the number of whole rounds less one (at least 1): the rounds before
   // the last keep each XCD's L2 sharing an expert's A and B blocks, and the
-  // last round and the split tail absorb what is uneven.  Otherwise S = 1.
+  // last round and the split tail absorb what is uneven.  When the tiles
+  // make whole rounds (W a multiple of G) nothing is uneven and every round
+  // is striped (S = W / G).  Otherwise S = 1.
   // Items past S*G take one ticket each (W - S*G of them when W > S*G) and
   // every worker with a first item (min(W, G) of them) draws one ticket past
   // the queue before it stops, so the worker that draws the last ticket,
@@ -556,8 +559,12 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // (dyn_base = S * G, recomputed where used: every value kept live through
   // the kernel costs registers the K loop needs.)
   auto dyn_base = [&]() -> int32_t {
-    if constexpr (kStaticRounds)
-      if (p.atomic && p.num_work < 0 && whole_m_tiles && W_tiles >= 2 * G) return (W_tiles / G - 1) * G;
+    if constexpr (kStaticRounds) {
+      if (p.atomic && p.num_work < 0 && whole_m_tiles && W_tiles >= 2 * G) {
+        if (W_tiles % G == 0) return W_tiles;
+        return (W_tiles / G - 1) * G;
+      }
+    }
     return G;
   };
   // Whether the item after `item` is drawn by ticket (else it is item + G):

@@ -138,8 +138,10 @@ def test_dirty_counter_word_is_reclaimed(cuda_device, poison):
 def test_atomic_static_rounds_on_whole_m_tiles(cuda_device, g_workers, poison):
     """Counts that fill whole 256-row m-tiles (every tile costs the same): the
     atomic schedule runs the rounds before the last in the striped placement
-    and draws tickets only after them.  12 tiles on 2, 3 and 4 workers (5, 3
-    and 2 static rounds) and on 5 (one static round, then tickets): every
+    (every round when the tiles make whole rounds) and draws tickets only
+    after them.  12 tiles on 2, 3 and 4 workers (6, 4 and 3 static rounds:
+    one ticket per worker past the queue) and on 5 (one static round, then
+    tickets): every
     tile once (oracle parity), the counter ends at W + G, also after a dirty
     counter word, and the results are bitwise the striped schedule's (K = 128
     is too short to split a tile: each part needs two 64-deep A blocks)."""
