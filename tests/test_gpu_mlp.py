@@ -98,7 +98,9 @@ def test_gather_rows_bit_exact(cuda_device):
 
 
 @pytest.mark.parametrize("H", [256, 13])
-@pytest.mark.parametrize("k", [1, 4, 10])  # 10: more slots than the kernel loads together
+# 1, 2: one slot at a time; 4, 10: slots loaded in groups of four (10: two
+# groups and a partial one)
+@pytest.mark.parametrize("k", [1, 2, 4, 10])
 def test_combine_matches_oracle(cuda_device, H, k):
     log(f"combine H={H} k={k}")
     T, E = 257, 12

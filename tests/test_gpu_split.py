@@ -70,7 +70,9 @@ def split_parts(w, g, k, gran=64):
 # 15: whole); K = 264: 3 tiles in halves of 128 and 136 (a partial stage);
 # K = 520: 3 tiles in quarters of 128, 128, 128 and 136; 28 tiles on 12
 # workers: the 4 past two rounds in thirds (3 * 4 <= 12 < 4 * 4), of K = 520
-# (128, 128, 264) and K = 400 (128, 128, 144).
+# (128, 128, 264) and K = 400 (128, 128, 144); 40 whole 256-row m-tiles on 12
+# workers: two static rounds (stripes, no ticket), then tickets for the third
+# round and the 4 tiles past it, in thirds.
 CASES = [([300, 0, 257, 1, 600], 1032, 520, 256),
          ([300, 0, 257, 1, 600], 1032, 520, 20),
          ([300, 0, 257, 1, 600], 1032, 520, 7),
@@ -78,8 +80,9 @@ CASES = [([300, 0, 257, 1, 600], 1032, 520, 256),
          ([64] * 3, 264, 256, 256),
          ([64] * 3, 520, 256, 256),
          ([256] * 27 + [5], 520, 256, 12),
-         ([256] * 27 + [5], 400, 256, 12)]
-EXPECT_PARTS = [4, 4, 2, 1, 2, 4, 3, 3]
+         ([256] * 27 + [5], 400, 256, 12),
+         ([256] * 40, 520, 256, 12)]
+EXPECT_PARTS = [4, 4, 2, 1, 2, 4, 3, 3, 3]
 
 
 @pytest.mark.parametrize("case", range(len(CASES)))
