@@ -140,11 +140,14 @@ int mgg_build_work_queue_host(const int64_t* expert_offsets, int64_t num_experts
  *   c  [M, N]     row stride ldc
  *   expert_offsets  int32 [E+1] on the device
  *
- * Work items are BLOCK_M x BLOCK_N output tiles in the queue order above.
+ * Work items are BLOCK_M x BLOCK_N output tiles.
  * work_expert/work_tile_m/work_tile_n (num_work entries, from
- * mgg_build_work_queue) are used when num_work >= 0; with num_work < 0 and
- * null queue pointers, the kernel derives the identical queue from the
- * offsets on the device (no host round trip).
+ * mgg_build_work_queue) are used, in their order, when num_work >= 0; with
+ * num_work < 0 and null queue pointers, the kernel derives the same tiles
+ * from the offsets on the device (no host round trip), ordered expert by
+ * expert and, within an expert, in groups of 4 m-tiles taken n-tile by
+ * n-tile (the group's m-tiles consecutive), so that each XCD's share of a
+ * round spans few A and B blocks.  A tile's sums do not depend on the order.
  *
  * num_workers persistent workgroups are launched (<= 0 means one per CU).
  * use_atomic_queue = 0: worker w takes items w, w+G, w+2G, ... (workers are

@@ -24,10 +24,13 @@ Differences, all in arguments that do not change results:
   order whatever the tile, so results do not depend on either choice.
 * ``block_k``, ``num_warps``, ``num_stages`` are accepted and ignored: the
   kernel's K staging, wave count and LDS ring are fixed by its design.
-* ``queue="device"`` (default) derives the same (expert, tile_m, tile_n) queue
-  inside the kernel from the offsets, so a call never waits on the device;
-  ``queue="prebuilt"`` goes through ``_build_work_queue`` (a host round trip
-  for the cache key, as in the reference).  Outputs are identical.  Above
+* ``queue="device"`` (default) derives the same (expert, tile_m, tile_n)
+  tiles inside the kernel from the offsets (an expert's m-tiles grouped by
+  four, each group taken n-tile by n-tile, for L2 reuse), so a call never
+  waits on the device; ``queue="prebuilt"`` goes through
+  ``_build_work_queue`` (a host round trip for the cache key, as in the
+  reference) and runs its row order.  Each tile's sums are the same either
+  way (the split last round below aside).  Above
   2048 experts (the device-derived queue keeps its tile prefix in LDS) the
   prebuilt path is taken without being asked.
 * ``work_counter`` (atomic mode) receives the final count W + G, the value
