@@ -154,9 +154,8 @@ int mgg_build_work_queue_host(const int64_t* expert_offsets, int64_t num_experts
  * numbered so that each XCD owns a contiguous slice of every round).
  * use_atomic_queue = 1: workers take the next item with an atomic add on a
  * 64-bit counter word (every worker's first item, and with the
- * device-derived queue and counts that fill whole block_m-row tiles its
- * items of every round but the last, or of every round when the tiles make
- * whole rounds, are its stripes, taken without a ticket).  The word is owned by the library: one per (device, stream) for
+ * device-derived queue and at least 2G tiles its items of every whole round,
+ * are its stripes, taken without a ticket; tickets serve the tail).  The word is owned by the library: one per (device, stream) for
  * direct launches, and one per (capture, stream) for launches captured into
  * a HIP graph (so graph replays never share a word with other launches; the
  * word is released when the graph is destroyed).  The words live in a

@@ -56,8 +56,8 @@
 #ifndef MGG_FULL_LOOP
 #define MGG_FULL_LOOP 1
 #endif
-// Atomic schedule on equal-cost tiles: whole rounds by the striped placement
-// (all rounds when the tiles make whole rounds, else all but the last).
+// Atomic schedule with the device-derived queue: every whole round of G tiles
+// by the striped placement, tickets only for the tail past them.
 #ifndef MGG_STATIC_ROUNDS
 #define MGG_STATIC_ROUNDS 1
 #endif
@@ -215,19 +215,17 @@ __device__ __forceinline__ float silu_mul(float gate, float up) {  // silu(gate)
 template <int BM, int NT>
 __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_prefix,
                                  int32_t* s_offs, int32_t* s_scan, int rep_tiles,
-                                 int32_t* w_report, bool* whole_m_tiles) {
+                                 int32_t* w_report) {
   const int tid = threadIdx.x;
   const int E = p.num_experts;
   const int per = (E + NT - 1) / NT;
   const int e0 = tid * per;
   int32_t local = 0;
   int64_t rep_local = 0;
-  int partial = 0;  // an expert whose last m-tile is partial
   for (int i = 0; i < per; ++i) {
     const int e = e0 + i;
     if (e < E) {
       const int64_t cnt = (int64_t)p.offsets[e + 1] - (int64_t)p.offsets[e];
-      partial |= cnt > 0 && cnt % BM != 0;
       const int64_t tiles = cnt > 0 ? ((cnt + BM - 1) / BM) * (int64_t)n_tiles : 0;
       local += (int32_t)tiles;
       if (rep_tiles > 0 && cnt > 0) rep_local += ((cnt + p.report_bm - 1) / p.report_bm) * (int64_t)rep_tiles;
@@ -272,7 +270,7 @@ __device__ int32_t derive_prefix(const GemmParams& p, int n_tiles, int32_t* s_pr
     s_prefix[E] = incl;
     if (s_offs != nullptr) s_offs[E] = p.offsets[E];
   }
-  *whole_m_tiles = __syncthreads_or(partial) == 0;
+  __syncthreads();
   const int32_t W = s_prefix[E];
   if (rep_tiles <= 0) *w_report = W;
   return W;
@@ -461,7 +459,7 @@ constexpr bool ablk_mode() {
 // current one.  `first` is this worker's first item (a ticket in atomic mode).
 template <int BM, int BN, int SBK, int NSTAGE, int NW, class T, int EPI>
 __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles, int32_t w_report,
-                                           bool whole_m_tiles, int32_t first, int n_tiles,
+                                           int32_t first, int n_tiles,
                                            const int32_t* s_prefix,
                                            const int32_t* s_offs, int32_t* s_item, uint8_t* lds,
                                            float* s_scale) {
@@ -540,14 +538,12 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   }
   // Atomic schedule: a worker's first S items are its stripes (items v, v+G,
   // ..., in the striped schedule's XCD-aware placement, no ticket), the rest
-  // go by tickets t of the global counter, standing for items S*G + t.  When
-  // every expert's rows fill whole m-tiles (all tiles cost alike, so the
-  // striped placement is balanced) and the queue is derived on the device, S
-  // is the number of whole rounds less one (at least 1): the rounds before
-  // the last keep each XCD's L2 sharing an expert's A and B blocks, and the
-  // last round and the split tail absorb what is uneven.  When the tiles
-  // make whole rounds (W a multiple of G) nothing is uneven and every round
-  // is striped (S = W / G).  Otherwise S = 1.
+  // go by tickets t of the global counter, standing for items S*G + t.  With
+  // the queue derived on the device and at least two rounds of tiles, S is
+  // the number of whole rounds (floor(W_tiles / G)): every whole round keeps
+  // each XCD's L2 sharing few A and B blocks (the queue's grouped order), and
+  // only the tail past them (the split parts, or whole tiles when the tail
+  // is too long to split) is drawn by ticket.  Otherwise S = 1.
   // Items past S*G take one ticket each (W - S*G of them when W > S*G) and
   // every worker with a first item (min(W, G) of them) draws one ticket past
   // the queue before it stops, so the worker that draws the last ticket,
@@ -562,13 +558,13 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // bookkeeping made it spill more for no gain there.)
   constexpr bool kStaticRounds = MGG_STATIC_ROUNDS && !(T::kScaled && BM == 256 && BN == 256);
   // (dyn_base = S * G, recomputed where used: every value kept live through
-  // the kernel costs registers the K loop needs.)
+  // the kernel costs registers the K loop needs.  Ticket-drawn tiles land on
+  // whichever XCD is free first, so their A and B blocks are fetched by
+  // several L2s; static rounds with partial m-tiles, whose costs differ,
+  // measured faster all the same: expert-MLP forward -1.1 to -2.8%.)
   auto dyn_base = [&]() -> int32_t {
     if constexpr (kStaticRounds) {
-      if (p.atomic && p.num_work < 0 && whole_m_tiles && W_tiles >= 2 * G) {
-        if (W_tiles % G == 0) return W_tiles;
-        return (W_tiles / G - 1) * G;
-      }
+      if (p.atomic && p.num_work < 0 && W_tiles >= 2 * G) return W_tiles / G * G;
     }
     return G;
   };
@@ -1751,13 +1747,12 @@ grouped_gemm_kernel(GemmParams p) {
   const int rep_tiles = rep_other ? (int)((p.n + p.report_bn - 1) / p.report_bn) : 0;
   int32_t w_report = 0;
   int32_t W;
-  bool whole_m_tiles = false;  // every expert's rows fill whole m-tiles: equal-cost tiles
   if (p.num_work >= 0) {
     W = p.num_work;
     w_report = rep_other ? queue_length<NT>(p, p.report_bm, rep_tiles, s_scan) : W;
   } else {
     W = derive_prefix<BM, NT>(p, n_tiles, s_prefix, kOffsLds ? s_offs : nullptr, s_scan,
-                              rep_tiles, &w_report, &whole_m_tiles);
+                              rep_tiles, &w_report);
   }
   if (W == 0) {
     // No ticket is drawn: the counter word is handed on to the next launch
@@ -1780,7 +1775,7 @@ grouped_gemm_kernel(GemmParams p) {
   // XCD-aware placement), then tickets t of the global counter stand for
   // items G + t; a worker stops at its first ticket past the queue.
   const int32_t first = v;
-  run_worker<BM, BN, SBK, NSTAGE, NW, T, EPI>(p, W, w_report, whole_m_tiles, first, n_tiles, s_prefix,
+  run_worker<BM, BN, SBK, NSTAGE, NW, T, EPI>(p, W, w_report, first, n_tiles, s_prefix,
                                          (kOffsLds && p.num_work < 0) ? s_offs : nullptr,
                                          s_item, lds, s_scale);
   if (probe) {

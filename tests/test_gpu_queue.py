@@ -133,22 +133,24 @@ def test_dirty_counter_word_is_reclaimed(cuda_device, poison):
             assert torch.equal(c2, out)
 
 
+@pytest.mark.parametrize("counts,tiles", [([512, 256, 0, 768], 12), ([300, 0, 257, 1, 600], 16)])
 @pytest.mark.parametrize("g_workers", [2, 3, 4, 5])
 @pytest.mark.parametrize("poison", [None, (9 << 32) | 5])
-def test_atomic_static_rounds_on_whole_m_tiles(cuda_device, g_workers, poison):
-    """Counts that fill whole 256-row m-tiles (every tile costs the same): the
-    atomic schedule runs the rounds before the last in the striped placement
-    (every round when the tiles make whole rounds) and draws tickets only
-    after them.  12 tiles on 2, 3 and 4 workers (6, 4 and 3 static rounds:
-    one ticket per worker past the queue) and on 5 (one static round, then
-    tickets): every
-    tile once (oracle parity), the counter ends at W + G, also after a dirty
-    counter word, and the results are bitwise the striped schedule's (K = 128
-    is too short to split a tile: each part needs two 64-deep A blocks)."""
-    counts, k, n = [512, 256, 0, 768], 128, 512
+def test_atomic_static_rounds(cuda_device, counts, tiles, g_workers, poison):
+    """With the device-derived queue and at least two rounds of tiles the
+    atomic schedule runs every whole round in the striped placement and
+    draws tickets only for the tail past them.  12 tiles (whole 256-row
+    m-tiles) on 2, 3 and 4 workers (6, 4 and 3 static rounds: one ticket per
+    worker past the queue) and on 5 (two static rounds, then 2 tiles by
+    ticket); 16 tiles with partial m-tiles on 2, 4 (8 and 4 rounds), 3 and 5
+    (5 and 3 rounds, then one tile by ticket): every tile once (oracle
+    parity), the counter ends at W + G, also after a dirty counter word, and
+    the results are bitwise the striped schedule's (K = 128 is too short to
+    split a tile: each part needs two 64-deep A blocks)."""
+    k, n = 128, 512
     a, b, offs = make_inputs(counts, k, n, torch.bfloat16, cuda_device, seed=11)
     w = queue_len(offs, n, 256, 256)
-    assert w == 12
+    assert w == tiles
     stream = torch.cuda.current_stream().cuda_stream
     striped = gg.persistent_grouped_gemm(a, b, offs, num_sms=g_workers, block_m=256, block_n=256,
                                          kernel_tile=(256, 256), use_atomic_queue=False)
@@ -156,7 +158,7 @@ def test_atomic_static_rounds_on_whole_m_tiles(cuda_device, g_workers, poison):
         if poison is not None:
             nat.check(nat.lib().mgg_debug_set_dequeue_counter(poison, stream))
         counter = torch.zeros(1, dtype=torch.int32, device=cuda_device)
-        log(f"static rounds G={g_workers} poison={poison} rep={rep}")
+        log(f"static rounds W={tiles} G={g_workers} poison={poison} rep={rep}")
         c = gg.persistent_grouped_gemm(a, b, offs, num_sms=g_workers, block_m=256, block_n=256,
                                        kernel_tile=(256, 256), work_counter=counter)
         torch.cuda.synchronize()
