@@ -197,18 +197,65 @@ layout_scatter_kernel(const In* idx, int64_t A, int32_t top_k, int32_t E, const 
 // counts in LDS; a prefix over the waves, per expert, then gives each wave's
 // base.  Positions are those of layout_scatter_kernel (assignment order
 // within each expert), with every assignment in flight at once.
+//
+// kScan (small layouts, nb * E <= kFusedScanMax): pass 2 runs inside this
+// pass instead of as its own launch.  `hist` then holds the count pass's
+// per-chunk counts as they are, and every workgroup derives its chunk's base
+// per expert from them: offsets[e] (an exclusive scan of the expert totals
+// over the whole table) plus the counts of the chunks before its own.
+// Workgroup 0 also writes counts and offsets.  The positions are the same.
 constexpr int kWideWaves = kLayoutChunk / 64;
 constexpr int kMaxWideExperts = 1024;  // [kWideWaves][E] int32 counters in 64 KiB of LDS
+constexpr int64_t kFusedScanMax = 16384;  // table entries every workgroup reads (64 KiB)
 
-template <class In>
+template <class In, bool kScan>
 __global__ void __launch_bounds__(kLayoutChunk)
 layout_scatter_wide_kernel(const In* idx, int64_t A, int32_t top_k, int32_t E,
-                           const int32_t* hist, int32_t* slot_pos, int32_t* token_index,
-                           int32_t* row_assign) {
+                           const int32_t* hist, int32_t nb, int32_t* counts, int32_t* offsets,
+                           int32_t* slot_pos, int32_t* token_index, int32_t* row_assign) {
   extern __shared__ int32_t s_cnt[];  // [kWideWaves][E]: counts, then bases
+  __shared__ int32_t s_base[kScan ? kMaxWideExperts : 1];  // kScan: chunk base per expert
+  __shared__ int32_t s_wsum[kScan ? kWideWaves : 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
+  if constexpr (kScan) {
+    // Thread x < E: expert x's total over all chunks and over the chunks
+    // before this one; then an exclusive scan of the totals (within each
+    // wave by shuffles, then over the wave sums).
+    int32_t total = 0, before = 0;
+    if (tid < E) {
+      for (int b0 = 0; b0 < nb; b0 += 8) {  // eight chunks' loads in flight at a time
+        int32_t c[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c[j] = b0 + j < nb ? hist[(int64_t)(b0 + j) * E + tid] : 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (b0 + j < (int)blockIdx.x) before += c[j];
+          total += c[j];
+        }
+      }
+    }
+    int32_t incl = total;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int32_t y = __shfl_up(incl, d);
+      if (lane >= d) incl += y;
+    }
+    if (lane == 63) s_wsum[w] = incl;
+    __syncthreads();
+    int32_t wbase = 0;
+    for (int v = 0; v < w; ++v) wbase += s_wsum[v];
+    const int32_t off = wbase + incl - total;  // offsets[tid]
+    if (tid < E) {
+      s_base[tid] = off + before;
+      if (blockIdx.x == 0) {
+        counts[tid] = total;
+        offsets[tid] = off;
+        if (tid == E - 1) offsets[E] = off + total;
+      }
+    }
+  }
   for (int i = tid; i < kWideWaves * E; i += kLayoutChunk) s_cnt[i] = 0;
   __syncthreads();
   const int64_t a = (int64_t)blockIdx.x * kLayoutChunk + tid;
@@ -231,7 +278,7 @@ layout_scatter_wide_kernel(const In* idx, int64_t A, int32_t top_k, int32_t E,
   }
   __syncthreads();
   for (int x = tid; x < E; x += kLayoutChunk) {
-    int32_t run = hist[(int64_t)blockIdx.x * E + x];
+    int32_t run = kScan ? s_base[x] : hist[(int64_t)blockIdx.x * E + x];
     for (int v = 0; v < kWideWaves; ++v) {
       const int32_t c = s_cnt[v * E + x];
       s_cnt[v * E + x] = run;
@@ -397,20 +444,28 @@ int launch_dispatch_layout(const void* topk_idx, int idx_type, int64_t num_token
     if (hipError_t err = hipGetLastError(); err != hipSuccess)
       return hip_error(err, "layout count launch");
   }
-  hipLaunchKernelGGL(layout_scan_kernel, dim3(1), dim3(kLayoutScanThreads), 0, stream, hist,
-                     (int32_t)nb, num_experts, counts, offsets);
-  if (hipError_t err = hipGetLastError(); err != hipSuccess)
-    return hip_error(err, "layout scan launch");
+  // Small layouts scan inside the position pass (one launch fewer).
+  const bool fused = nb > 0 && num_experts > 0 && num_experts <= kMaxWideExperts &&
+                     nb * (int64_t)num_experts <= kFusedScanMax;
+  if (!fused) {
+    hipLaunchKernelGGL(layout_scan_kernel, dim3(1), dim3(kLayoutScanThreads), 0, stream, hist,
+                       (int32_t)nb, num_experts, counts, offsets);
+    if (hipError_t err = hipGetLastError(); err != hipSuccess)
+      return hip_error(err, "layout scan launch");
+  }
   if (nb > 0 && num_experts <= kMaxWideExperts) {
     const size_t wide_lds = (size_t)kWideWaves * lds;
-    if (idx_type == MGG_INT64)
-      hipLaunchKernelGGL(layout_scatter_wide_kernel<int64_t>, dim3((unsigned)nb),
-                         dim3(kLayoutChunk), wide_lds, stream, (const int64_t*)topk_idx, A, top_k,
-                         num_experts, hist, slot_pos, token_index, row_assign);
-    else
-      hipLaunchKernelGGL(layout_scatter_wide_kernel<int32_t>, dim3((unsigned)nb),
-                         dim3(kLayoutChunk), wide_lds, stream, (const int32_t*)topk_idx, A, top_k,
-                         num_experts, hist, slot_pos, token_index, row_assign);
+#define MGG_WIDE(IN, SCAN)                                                                     \
+  hipLaunchKernelGGL((layout_scatter_wide_kernel<IN, SCAN>), dim3((unsigned)nb),                \
+                     dim3(kLayoutChunk), wide_lds, stream, (const IN*)topk_idx, A, top_k,        \
+                     num_experts, hist, (int32_t)nb, counts, offsets, slot_pos, token_index,     \
+                     row_assign)
+    if (idx_type == MGG_INT64) {
+      if (fused) MGG_WIDE(int64_t, true); else MGG_WIDE(int64_t, false);
+    } else {
+      if (fused) MGG_WIDE(int32_t, true); else MGG_WIDE(int32_t, false);
+    }
+#undef MGG_WIDE
     if (hipError_t err = hipGetLastError(); err != hipSuccess)
       return hip_error(err, "layout scatter launch");
   } else if (nb > 0) {

@@ -44,12 +44,17 @@ def random_routing(T, k, E, masked_every=0, seed=0, dtype=torch.int64):
     return idx.to(dtype), w
 
 
+# (T, k, E, masked_every).  Paths: no assignments; the position pass with
+# the scan inside it (chunks x experts <= 16384: the next four); the
+# separate scan with the wide position pass (157 chunks x 256 experts); the
+# one-wave position pass (E > 1024).
 LAYOUT_CASES = [
     (0, 2, 4, 0),
     (1, 1, 1, 0),
     (37, 3, 5, 4),
     (1500, 2, 3, 0),
     (3000, 4, 300, 9),
+    (20000, 8, 256, 7),
     (700, 8, 8192, 5),
 ]
 
