@@ -71,6 +71,11 @@
 #define MGG_BSTREAM 1
 #endif
 // Most parts a tile of a short last round is split into.
+// Split last round: each K part at least this deep (a part's meetings cost
+// about as much as 1024 of K on the 256x256 tile).
+#ifndef MGG_SPLIT_MIN_K
+#define MGG_SPLIT_MIN_K 1024
+#endif
 #ifndef MGG_SPLIT_MAX
 #define MGG_SPLIT_MAX 4
 #endif
@@ -520,16 +525,20 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // + s*t + q is part q of tile w_base + t); W counts work items.  The parts
   // meet pairwise in split_fixup.  A granule is an A block (A-block tile) or
   // a stage, so every part starts on a stage boundary; each part holds at
-  // least two.  The striped schedule keeps whole tiles.
+  // least MGG_SPLIT_MIN_K of K (the meetings, about 7-20 µs a tree level
+  // depending on the card, outweigh shorter parts: with K = 2048 halves
+  // measured 1.5-1.9% faster than quarters on the skewed workload).  The
+  // striped schedule keeps whole tiles.
   constexpr int kGran = kABlk ? 2 * kBK : kBK;
   const int n_gran = (int)((K + kGran - 1) / kGran);
+  constexpr int kMinPartGran = (MGG_SPLIT_MIN_K + kGran - 1) / kGran;
   int32_t w_base = W_tiles;
   int32_t W = W_tiles;
   int split_s = 1;  // parts per split tile
   if (p.atomic && p.num_work < 0 && p.split_flags != nullptr) {
     const int32_t rem = W_tiles > G ? W_tiles % G : W_tiles;
     for (int sp = MGG_SPLIT_MAX; sp >= 2 && split_s == 1; --sp)
-      if (rem > 0 && (int64_t)rem * sp <= G && (int64_t)rem * sp <= p.split_slots && n_gran >= 2 * sp)
+      if (rem > 0 && (int64_t)rem * sp <= G && (int64_t)rem * sp <= p.split_slots && n_gran >= kMinPartGran * sp)
         split_s = sp;
     if (split_s > 1) {
       w_base = W_tiles - rem;

@@ -67,7 +67,7 @@ def test_n_not_multiple_of_8(cuda_device, n, dtype, layout):
     if layout == "k_major":
         b = b.transpose(1, 2).contiguous().transpose(1, 2)
     want = oracle(a, b, offs)
-    for atomic in (False, True):  # (the atomic launches split their short last round)
+    for atomic in (False, True):
         log(f"N={n} {dtype} {layout} atomic={atomic}")
         c = gg.persistent_grouped_gemm(a, b, offs, use_atomic_queue=atomic)
         torch.cuda.synchronize()
@@ -197,8 +197,9 @@ def test_odd_n_split_tiles(cuda_device, counts, num_sms):
     """The atomic schedule's split last round with odd N (256x256 tiles, one
     n-tile): 5 tiles on 4 workers take the last one, the last expert's, in 4
     K parts; 5 on 2 in 2 parts; 4 on 3 in 3 parts; 2 on 8 both in 4 parts.
-    The last part's descriptor stops at B's last element."""
-    k, n = 1032, 201
+    The last part's descriptor stops at B's last element (K = 4104: each part
+    at least 1024 deep)."""
+    k, n = 4104, 201
     a, b, offs = last_element_inputs(counts, k, n, torch.bfloat16, cuda_device, seed=num_sms)
     want = oracle(a, b, offs)
     log(f"odd N split counts={counts} num_sms={num_sms}")

@@ -146,7 +146,7 @@ def test_atomic_static_rounds(cuda_device, counts, tiles, g_workers, poison):
     (5 and 3 rounds, then one tile by ticket): every tile once (oracle
     parity), the counter ends at W + G, also after a dirty counter word, and
     the results are bitwise the striped schedule's (K = 128 is too short to
-    split a tile: each part needs two 64-deep A blocks)."""
+    split a tile: each part needs 1024 of K)."""
     k, n = 128, 512
     a, b, offs = make_inputs(counts, k, n, torch.bfloat16, cuda_device, seed=11)
     w = queue_len(offs, n, 256, 256)
@@ -169,9 +169,10 @@ def test_atomic_static_rounds(cuda_device, counts, tiles, g_workers, poison):
 
 def test_atomic_launches_on_two_streams_at_once(cuda_device):
     """Atomic launches on two created streams run concurrently on separate
-    counter words and split-tile workspaces; every result matches the serial
-    one bitwise."""
-    cases = [make_inputs([300, 5, 0, 600], 256, 512, torch.bfloat16, cuda_device, seed=s)
+    counter words and split-tile workspaces (12 tiles on 128 and 192
+    workers, each split in halves of K = 2056); every result matches the
+    serial one bitwise."""
+    cases = [make_inputs([300, 5, 0, 600], 2056, 512, torch.bfloat16, cuda_device, seed=s)
              for s in (1, 2)]
     refs = [gg.persistent_grouped_gemm(a, b, o, num_sms=128 + 64 * i, use_atomic_queue=True)
             for i, (a, b, o) in enumerate(cases)]
@@ -187,7 +188,7 @@ def test_atomic_launches_on_two_streams_at_once(cuda_device):
     for i in range(2):
         for got in outs[i]:
             assert torch.equal(got, refs[i])
-    assert_parity(refs[0], *cases[0], 256)
+    assert_parity(refs[0], *cases[0], 2056)
 
 
 def test_graph_capture_and_replay(cuda_device):

@@ -53,35 +53,36 @@ def tiles(counts, n, bm, bn):
     return sum((c + bm - 1) // bm for c in counts if c > 0) * ((n + bn - 1) // bn)
 
 
-def split_parts(w, g, k, gran=64):
+def split_parts(w, g, k, gran=64, min_k=1024):
     """(tiles split, parts per tile) of the atomic schedule's last round: the
-    most parts s in (4, 3, 2) with s * rem <= g and at least two K granules
-    (64-deep A blocks of the 256x256 tile) per part."""
+    most parts s in (4, 3, 2) with s * rem <= g and at least min_k of K per
+    part (16 granules, the 64-deep A blocks of the 256x256 tile)."""
     rem = w % g if w > g else w
     n_gran = -(-k // gran)
     for s in (4, 3, 2):
-        if 0 < rem and s * rem <= g and n_gran >= 2 * s:
+        if 0 < rem and s * rem <= g and n_gran >= -(-min_k // gran) * s:
             return rem, s
     return 0, 1
 
 
 # (counts, K, N, workers): 24 tiles of 256x256 on 256 workers (all split in
 # 4), on 20 (4 tiles past the full round, in 4), 7 (3 tiles in 2), 30 (24 >
-# 15: whole); K = 264: 3 tiles in halves of 128 and 136 (a partial stage);
-# K = 520: 3 tiles in quarters of 128, 128, 128 and 136; 28 tiles on 12
-# workers: the 4 past two rounds in thirds (3 * 4 <= 12 < 4 * 4), of K = 520
-# (128, 128, 264) and K = 400 (128, 128, 144); 40 whole 256-row m-tiles on 12
-# workers: two static rounds (stripes, no ticket), then tickets for the third
-# round and the 4 tiles past it, in thirds.
-CASES = [([300, 0, 257, 1, 600], 1032, 520, 256),
-         ([300, 0, 257, 1, 600], 1032, 520, 20),
-         ([300, 0, 257, 1, 600], 1032, 520, 7),
-         ([300, 0, 257, 1, 600], 1032, 520, 30),
-         ([64] * 3, 264, 256, 256),
-         ([64] * 3, 520, 256, 256),
-         ([256] * 27 + [5], 520, 256, 12),
-         ([256] * 27 + [5], 400, 256, 12),
-         ([256] * 40, 520, 256, 12)]
+# 15: whole); K = 2056: 3 tiles in halves of 1024 and 1032 (a partial
+# stage); K = 4104: 3 tiles in quarters of 1024, 1024, 1024 and 1032; 28
+# tiles on 12 workers: two static rounds, then the 4 tiles past them in
+# thirds (3 * 4 <= 12 < 4 * 4), of K = 3144 (1024, 1088, 1032) and K = 3100
+# (1024, 1024, 1052); 40 whole 256-row m-tiles on 12 workers: three static
+# rounds (stripes, no ticket), then the 4 tiles past them in thirds.  (Each
+# part holds at least 1024 of K.)
+CASES = [([300, 0, 257, 1, 600], 4104, 520, 256),
+         ([300, 0, 257, 1, 600], 4104, 520, 20),
+         ([300, 0, 257, 1, 600], 4104, 520, 7),
+         ([300, 0, 257, 1, 600], 4104, 520, 30),
+         ([64] * 3, 2056, 256, 256),
+         ([64] * 3, 4104, 256, 256),
+         ([256] * 27 + [5], 3144, 256, 12),
+         ([256] * 27 + [5], 3100, 256, 12),
+         ([256] * 40, 3144, 256, 12)]
 EXPECT_PARTS = [4, 4, 2, 1, 2, 4, 3, 3, 3]
 
 
@@ -117,7 +118,7 @@ def test_split_last_round(cuda_device, case, dtype):
 def test_split_flags_left_dirty(cuda_device, poison):
     """Flag words left at any value (as a launch that did not finish could
     leave them) neither lose a half's partial sums nor add them twice."""
-    counts, k, n = [300, 0, 257, 1, 600], 1032, 520
+    counts, k, n = [300, 0, 257, 1, 600], 4104, 520
     a, b, offs = make_inputs(counts, k, n, torch.bfloat16, cuda_device, seed=3)
     stream = torch.cuda.current_stream().cuda_stream
     clean = gg.persistent_grouped_gemm(a, b, offs)  # also creates this stream's split workspace
@@ -134,7 +135,7 @@ def test_split_flags_left_dirty(cuda_device, poison):
 def test_split_kmajor_b_matches_nmajor(cuda_device):
     """K-major B (a [E, K, N] view of [E, N, K] memory) splits at the same K
     and gives the same bits as N-major B."""
-    counts, k, n = [300, 0, 257, 1, 600], 1032, 520
+    counts, k, n = [300, 0, 257, 1, 600], 4104, 520
     a, b, offs = make_inputs(counts, k, n, torch.bfloat16, cuda_device, seed=4)
     b_km = b.transpose(1, 2).contiguous().transpose(1, 2)
     for tile in ((256, 256), (128, 128)):
@@ -146,10 +147,10 @@ def test_split_kmajor_b_matches_nmajor(cuda_device):
 
 
 def test_split_fp8(cuda_device):
-    """fp8 (12 tiles of 256x256, K = 1024: quarters of two 128-deep stages):
+    """fp8 (12 tiles of 256x256, K = 4096: quarters of eight 128-deep stages):
     the parts' sums are unscaled; the worker that completes the last meeting
     applies the row and column scales once, after adding them."""
-    counts, k, n = [300, 5, 0, 600], 1024, 384
+    counts, k, n = [300, 5, 0, 600], 4096, 384
     gen = torch.Generator().manual_seed(11)
     x = torch.randn(sum(counts), k, generator=gen)
     wt = torch.randn(len(counts), n, k, generator=gen) / math.sqrt(k)
@@ -236,7 +237,7 @@ def test_split_workspace_is_one_slot_per_cu(cuda_device):
     flag word per CU, whatever the worker count: 64 MiB on a 256-CU device
     after a num_sms=1000 call (24 tiles in 4 parts), and reserving it again
     changes nothing."""
-    counts, k, n = [300, 0, 257, 1, 600], 1032, 520
+    counts, k, n = [300, 0, 257, 1, 600], 4104, 520
     a, b, offs = make_inputs(counts, k, n, torch.bfloat16, cuda_device, seed=2)
     gg.reserve_split_workspace(cuda_device)
     c = gg.persistent_grouped_gemm(a, b, offs, num_sms=1000)

@@ -77,17 +77,21 @@ def test_meetings_store_each_tile_once(s):
 
 
 @pytest.mark.parametrize("s", [2, 3, 4])
-def test_k_parts_cover_k(s):
-    gran = 64
-    for k in range(1, 9000, 13):
+@pytest.mark.parametrize("gran", [32, 64, 128])
+def test_k_parts_cover_k(s, gran):
+    """Parts are taken only when each holds at least 1024 of K (as many
+    granules as that takes); they then tile [0, K) and each is at least
+    1024 - gran + 1 deep (its last granule possibly partial)."""
+    min_gran = -(-1024 // gran)
+    for k in range(1, 20000, 13):
         n_gran = -(-k // gran)
-        if n_gran < 2 * s:
+        if n_gran < min_gran * s:
             continue
         ends = []
         for q in range(s):
             kb = (q * n_gran // s) * gran
             ke = k if q == s - 1 else ((q + 1) * n_gran // s) * gran
-            assert ke - kb > gran  # two granules, the last possibly partial
+            assert ke - kb > (min_gran - 1) * gran
             ends.append((kb, ke))
         assert ends[0][0] == 0 and ends[-1][1] == k
         assert all(ends[i][1] == ends[i + 1][0] for i in range(s - 1))
