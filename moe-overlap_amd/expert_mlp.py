@@ -8,9 +8,11 @@ The reference runs its experts as (src/train_moe_baseline.py:212-248, :335-341):
     out += y * gate                     (once per top-k slot)
 
 Here all T*k assignments go through in one pass, with no host
-synchronisation: the dispatch layout, the row gather, the up-projection GEMM
-with the activation fused into its epilogue, the down-projection GEMM and the
-gate-weighted combine are five launches on the current stream.  Buffers are
+synchronisation: the dispatch layout (two kernels), the up-projection GEMM
+reading its rows through the layout (the row gather fused; a separate gather
+launch for shapes the fused path does not take) with the activation fused
+into its epilogue, the down-projection GEMM and the gate-weighted combine:
+five launches on the current stream.  Buffers are
 sized for T*k rows; the kernels read the number of valid rows (offsets[E])
 on the device.  Every op runs in libmgg.so (include/mgg.h); there is no
 fallback implementation.
