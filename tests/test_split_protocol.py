@@ -79,19 +79,31 @@ def test_meetings_store_each_tile_once(s):
 @pytest.mark.parametrize("s", [2, 3, 4])
 @pytest.mark.parametrize("gran", [32, 64, 128])
 def test_k_parts_cover_k(s, gran):
-    """Parts are taken only when each holds at least 1024 of K (as many
-    granules as that takes); they then tile [0, K) and each is at least
-    1024 - gran + 1 deep (its last granule possibly partial)."""
+    """Parts are taken only when an even cut would give each at least 1024 of
+    K (as many granules as that takes); they then tile [0, K).  Thirds and
+    quarters are even (each at least 1024 - gran + 1 deep, its last granule
+    possibly partial); halves are cut 384 of K (rounded up to granules)
+    longer for part 0, and part 1 keeps more than 1024 - 384 - 2 gran."""
     min_gran = -(-1024 // gran)
+    stagger = -(-384 // gran)
+
+    def bound(p, n_gran):
+        return (n_gran + stagger) // 2 if s == 2 else p * n_gran // s
+
     for k in range(1, 20000, 13):
         n_gran = -(-k // gran)
         if n_gran < min_gran * s:
             continue
         ends = []
         for q in range(s):
-            kb = (q * n_gran // s) * gran
-            ke = k if q == s - 1 else ((q + 1) * n_gran // s) * gran
-            assert ke - kb > (min_gran - 1) * gran
+            kb = 0 if q == 0 else bound(q, n_gran) * gran
+            ke = k if q == s - 1 else bound(q + 1, n_gran) * gran
+            if s == 2:
+                assert ke - kb > 1024 - 384 - 2 * gran
+            else:
+                assert ke - kb > (min_gran - 1) * gran
             ends.append((kb, ke))
+        if s == 2:
+            assert ends[0][1] - ends[0][0] >= ends[1][1] - ends[1][0] + stagger * gran - gran
         assert ends[0][0] == 0 and ends[-1][1] == k
         assert all(ends[i][1] == ends[i + 1][0] for i in range(s - 1))
