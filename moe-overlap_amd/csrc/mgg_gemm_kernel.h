@@ -536,12 +536,14 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   constexpr int kGran = kABlk ? 2 * kBK : kBK;
   const int n_gran = (int)((K + kGran - 1) / kGran);
   constexpr int kMinPartGran = (MGG_SPLIT_MIN_K + kGran - 1) / kGran;
-  // Halves (s = 2) are cut unevenly: part 0 takes kSplitStagger granules
-  // more than part 1, so part 1 reaches the meeting first and writes its
-  // sums while part 0 still runs K steps; part 0 then finds them complete
-  // and only reads (with even halves both arrive together and both write).
-  // 384 of K measured best (skewed atomic -1.7 to -1.9% against even
-  // halves, up GEMM -0.6%; 512 and more slower again).
+  // Parts are cut unevenly: at every meeting of the tree the higher subtree
+  // (the one whose parts have that level's bit set) should arrive first and
+  // write its sums while the lower one still runs K steps, so that the
+  // lower one only reads (parts of even length arrive together and both
+  // write).  Part q gets kSplitStagger granules less per bit set in q.
+  // 384 of K measured best for halves (skewed atomic -1.7 to -1.9% against
+  // even halves, up GEMM -0.6%; 512 and more slower again); thirds with it,
+  // the down GEMM -0.7%.
   constexpr int kSplitStagger = (MGG_SPLIT_STAGGER_K + kGran - 1) / kGran;
   int32_t w_base = W_tiles;
   int32_t W = W_tiles;
@@ -754,9 +756,16 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
     int kb = 0, klen = (int)K;
     if (c.slot >= 0) {
       const int q = c.slot % split_s;
-      // Granule boundary before part p (p = 1 .. s-1); halves are staggered.
+      // Granule boundary before part pb (pb = 1 .. s-1): part q's share is
+      // c - d * popcount(q) granules, c = (n_gran + d * P) / s, where d =
+      // kSplitStagger and P sums popcount(q) over the s parts (see there).
+      auto pc_sum = [](int pb) {  // popcount(0) + ... + popcount(pb - 1)
+        int t = 0;
+        for (int j = 1; j < pb; ++j) t += __builtin_popcount(j);
+        return t;
+      };
       auto bound = [&](int pb) {
-        return split_s == 2 ? (n_gran + kSplitStagger) / 2 : pb * n_gran / split_s;
+        return pb * (n_gran + kSplitStagger * pc_sum(split_s)) / split_s - kSplitStagger * pc_sum(pb);
       };
       kb = q == 0 ? 0 : bound(q) * kGran;
       const int ke = q == split_s - 1 ? (int)K : bound(q + 1) * kGran;

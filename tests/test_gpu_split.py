@@ -67,14 +67,14 @@ def split_parts(w, g, k, gran=64, min_k=1024):
 
 # (counts, K, N, workers): 24 tiles of 256x256 on 256 workers (all split in
 # 4), on 20 (4 tiles past the full round, in 4), 7 (3 tiles in 2), 30 (24 >
-# 15: whole); K = 2056: 3 tiles in halves of 1216 and 840 (halves are cut
-# 384 apart; a partial stage); K = 4104: 3 tiles in quarters of 1024, 1024,
-# 1024 and 1032; 28
+# 15: whole); K = 2056: 3 tiles in halves of 1216 and 840 (a partial
+# stage); K = 4104: 3 tiles in quarters of 1408, 1024, 1024 and 648; 28
 # tiles on 12 workers: two static rounds, then the 4 tiles past them in
-# thirds (3 * 4 <= 12 < 4 * 4), of K = 3144 (1024, 1088, 1032) and K = 3100
-# (1024, 1024, 1052); 40 whole 256-row m-tiles on 12 workers: three static
+# thirds (3 * 4 <= 12 < 4 * 4), of K = 3144 (1280, 960, 904) and K = 3100
+# (1280, 896, 924); 40 whole 256-row m-tiles on 12 workers: three static
 # rounds (stripes, no ticket), then the 4 tiles past them in thirds.  (An
-# even cut would give each part at least 1024 of K.)
+# even cut would give each part at least 1024 of K; part q is cut 384 of K
+# shorter per bit set in q.)
 CASES = [([300, 0, 257, 1, 600], 4104, 520, 256),
          ([300, 0, 257, 1, 600], 4104, 520, 20),
          ([300, 0, 257, 1, 600], 4104, 520, 7),

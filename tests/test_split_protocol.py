@@ -80,15 +80,18 @@ def test_meetings_store_each_tile_once(s):
 @pytest.mark.parametrize("gran", [32, 64, 128])
 def test_k_parts_cover_k(s, gran):
     """Parts are taken only when an even cut would give each at least 1024 of
-    K (as many granules as that takes); they then tile [0, K).  Thirds and
-    quarters are even (each at least 1024 - gran + 1 deep, its last granule
-    possibly partial); halves are cut 384 of K (rounded up to granules)
-    longer for part 0, and part 1 keeps more than 1024 - 384 - 2 gran."""
+    K (as many granules as that takes); they then tile [0, K), and part q is
+    d granules (384 of K, rounded up) shorter per bit set in q than part 0,
+    to within a granule of rounding (the last part's last granule possibly
+    partial), every part keeping more than a quarter of 1024."""
     min_gran = -(-1024 // gran)
-    stagger = -(-384 // gran)
+    d = -(-384 // gran)
+
+    def pc_sum(p):
+        return sum(bin(j).count("1") for j in range(1, p))
 
     def bound(p, n_gran):
-        return (n_gran + stagger) // 2 if s == 2 else p * n_gran // s
+        return p * (n_gran + d * pc_sum(s)) // s - d * pc_sum(p)
 
     for k in range(1, 20000, 13):
         n_gran = -(-k // gran)
@@ -98,12 +101,12 @@ def test_k_parts_cover_k(s, gran):
         for q in range(s):
             kb = 0 if q == 0 else bound(q, n_gran) * gran
             ke = k if q == s - 1 else bound(q + 1, n_gran) * gran
-            if s == 2:
-                assert ke - kb > 1024 - 384 - 2 * gran
-            else:
-                assert ke - kb > (min_gran - 1) * gran
+            assert ke - kb > 256
             ends.append((kb, ke))
-        if s == 2:
-            assert ends[0][1] - ends[0][0] >= ends[1][1] - ends[1][0] + stagger * gran - gran
+        g0 = ends[0][1] - ends[0][0]
+        for q in range(1, s):
+            gq = ends[q][1] - ends[q][0]
+            want = g0 - d * gran * bin(q).count("1")
+            assert abs(gq - want) <= 2 * gran, (k, q, gq, want)
         assert ends[0][0] == 0 and ends[-1][1] == k
         assert all(ends[i][1] == ends[i + 1][0] for i in range(s - 1))
