@@ -70,15 +70,16 @@
 #ifndef MGG_BSTREAM
 #define MGG_BSTREAM 1
 #endif
-// Most parts a tile of a short last round is split into.
-// Split last round: each K part at least this deep (a part's meetings cost
-// about as much as 1024 of K on the 256x256 tile).
+// Split last round: each K part of an even cut at least this deep (a
+// part's meetings cost about as much as 1024 of K on the 256x256 tile).
 #ifndef MGG_SPLIT_MIN_K
 #define MGG_SPLIT_MIN_K 1024
 #endif
+// Split last round: K by which part q is cut shorter per bit set in q.
 #ifndef MGG_SPLIT_STAGGER_K
 #define MGG_SPLIT_STAGGER_K 384
 #endif
+// Most parts a tile of a short last round is split into.
 #ifndef MGG_SPLIT_MAX
 #define MGG_SPLIT_MAX 4
 #endif
@@ -522,14 +523,14 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // When the rem tiles past the last full round of G are at most G/s for
   // some s in 2 .. MGG_SPLIT_MAX (the largest such s is taken; the library
   // provided the partial-sum workspace), each of them becomes s work items,
-  // the parts q = 0 .. s-1 of K, [K_q, K_q+1) with K_q = floor(q * n_gran /
-  // s) granules, taken by s workers: the last round runs on s times as many
-  // CUs for 1/s as long.  Queue items past w_base are the parts (item w_base
-  // + s*t + q is part q of tile w_base + t; halves are cut unevenly, see
-  // kSplitStagger); W counts work items.  The parts
+  // the parts q = 0 .. s-1 of K, [K_q, K_q+1) in whole granules (cut
+  // unevenly, see kSplitStagger), taken by s workers: the last round runs on
+  // s times as many CUs for about 1/s as long.  Queue items past w_base are
+  // the parts (item w_base + s*t + q is part q of tile w_base + t); W counts
+  // work items.  The parts
   // meet pairwise in split_fixup.  A granule is an A block (A-block tile) or
   // a stage, so every part starts on a stage boundary; each part holds at
-  // least MGG_SPLIT_MIN_K of K (the meetings, about 7-20 µs a tree level
+  // least MGG_SPLIT_MIN_K of K in an even cut (the meetings, about 7-20 µs a tree level
   // depending on the card, outweigh shorter parts: with K = 2048 halves
   // measured 1.5-1.9% faster than quarters on the skewed workload).  The
   // striped schedule keeps whole tiles.
