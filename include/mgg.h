@@ -310,8 +310,9 @@ int mgg_debug_set_split_flags(uint64_t value, void* stream);
  * (its atomic kernel takes whole items).  With the device-derived queue, an
  * atomic launch whose last round holds at most a quarter (a third, a half)
  * as many tiles as workers takes each of those tiles as 4 (3, 2) parts of K
- * (each part at least 1024 deep in K, so K >= 2048 for halves, 3072 for
- * thirds, 4096 for quarters); the parts'
+ * (each part of an even cut at least 1024 deep in K, so K >= 2048 for
+ * halves, 3072 for thirds, 4096 for quarters; twice that for fp8); the
+ * parts'
  * fp32 sums meet in a per-(device, stream) workspace of one 256 x 256 fp32
  * slot per CU (64 MiB on a 256-CU device) plus one flag word per CU.  The
  * sums then round differently in the last bits from the unsplit tile

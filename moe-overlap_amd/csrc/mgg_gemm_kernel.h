@@ -536,7 +536,10 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // striped schedule keeps whole tiles.
   constexpr int kGran = kABlk ? 2 * kBK : kBK;
   const int n_gran = (int)((K + kGran - 1) / kGran);
-  constexpr int kMinPartGran = (MGG_SPLIT_MIN_K + kGran - 1) / kGran;
+  // (Both in 16-bit K: fp8 parts are twice as deep, its MFMAs taking half
+  // the time per K; fp8 256x128 at K = 2048 in halves ran 7.9% slower than
+  // whole tiles.)
+  constexpr int kMinPartGran = (MGG_SPLIT_MIN_K * 2 / kE + kGran - 1) / kGran;
   // Parts are cut unevenly: at every meeting of the tree the higher subtree
   // (the one whose parts have that level's bit set) should arrive first and
   // write its sums while the lower one still runs K steps, so that the
@@ -545,7 +548,7 @@ __device__ __forceinline__ void run_worker(const GemmParams& p, int32_t W_tiles,
   // 384 of K measured best for halves (skewed atomic -1.7 to -1.9% against
   // even halves, up GEMM -0.6%; 512 and more slower again); thirds with it,
   // the down GEMM -0.7%.
-  constexpr int kSplitStagger = (MGG_SPLIT_STAGGER_K + kGran - 1) / kGran;
+  constexpr int kSplitStagger = (MGG_SPLIT_STAGGER_K * 2 / kE + kGran - 1) / kGran;
   int32_t w_base = W_tiles;
   int32_t W = W_tiles;
   int split_s = 1;  // parts per split tile

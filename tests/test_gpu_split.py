@@ -148,10 +148,10 @@ def test_split_kmajor_b_matches_nmajor(cuda_device):
 
 
 def test_split_fp8(cuda_device):
-    """fp8 (12 tiles of 256x256, K = 4096: quarters of eight 128-deep stages):
+    """fp8 (12 tiles of 256x256, K = 8192: quarters, each at least 2048 deep):
     the parts' sums are unscaled; the worker that completes the last meeting
     applies the row and column scales once, after adding them."""
-    counts, k, n = [300, 5, 0, 600], 4096, 384
+    counts, k, n = [300, 5, 0, 600], 8192, 384
     gen = torch.Generator().manual_seed(11)
     x = torch.randn(sum(counts), k, generator=gen)
     wt = torch.randn(len(counts), n, k, generator=gen) / math.sqrt(k)
