@@ -1,5 +1,5 @@
 """CPU model of the atomic schedule's split last round (the meeting protocol of
-split_fixup in moe-overlap_amd/csrc/mgg_gemm.hip), run over random
+split_fixup in moe-overlap_amd/csrc/mgg_gemm_kernel.h), run over random
 interleavings of the parts.
 
 The kernel's part q of split tile t (s parts, any s >= 2) meets its siblings in
@@ -11,7 +11,7 @@ takes a ticket (0: done; 1: winner).  The winner adds the sibling's slot and
 goes on.  Checked: exactly one worker stores each tile and it holds every part
 once, no slot is read before its writer finished or overwritten before it is
 read, flag indices stay inside the tile's s - 1 words and slot indices inside
-its s, and the K parts cover [0, K) with at least two granules each.  The
+its s, and the K parts (cut unevenly) cover [0, K).  The
 reference takes whole tiles (src/triton_grouped_gemm.py:157-233); this models
 this build's own protocol.
 """
